@@ -1,0 +1,343 @@
+#!/usr/bin/env python3
+"""Benchmark of the Q4_0 ring decode-attention path on one MI355X.
+
+Default workload: one step = decode attention of 64
+sessions through 32 layers (32 launches), 32 heads x head_dim 128, full
+W=512 windows at per-session positions drawn from U[512, 4096), K/V from
+N(0,1) with each element scaled x8 with probability 1%, quantized to Q4_0 by
+the library's own append kernel.  The ring (4.83 GB) is resident in HBM
+before timing starts.
+
+value = algorithmic bytes per step / step time, where the algorithmic bytes
+of one (session, layer) are the full window's Q4_0 K+V bytes
+(W*H*2*(D/32)*18) plus q and out in fp32 (2*H*D*4): 2,392,064 B, so
+4,898,947,072 B per step.
+
+Also reported: B=1 latency (one layer, 32 heads, W=512,
+write head at position 700; fused append+decode as the reference kernel does,
+and decode alone), per-launch durations of the dominant kernel from HIP
+events recorded on the launch stream inside the timed region (roofline), and
+the CPU baseline (the oracle's fp32 restatement of the reference CPU path,
+timed on this host on a bounded sample of the same ring).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg3|cfg4]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+METRIC = "Q4_0 KV GB/s + % of 8 TB/s HBM at B=64 W=512 32L; µs/layer at B=1"
+HBM_PEAK_GBS = 8000.0
+
+
+def unit_bytes(H, D, W):
+    """Algorithmic bytes of one (session, layer) decode."""
+    return W * H * 2 * (D // 32) * 18 + 2 * H * D * 4
+
+
+def fused_extra_bytes(H, D):
+    """New K/V fp32 rows read plus their Q4_0 blocks written, per (session, layer)."""
+    return 2 * H * D * 4 + 2 * H * (D // 32) * 18
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def fill_ring(torch, ring, L, S, H, D, W, pos_host, seed, outlier_p=0.01):
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    stream = torch.cuda.current_stream()
+    for layer in range(L):
+        k = torch.randn((S, W, H, D), device="cuda", generator=gen)
+        v = torch.randn((S, W, H, D), device="cuda", generator=gen)
+        if outlier_p > 0:
+            k.mul_(torch.where(torch.rand((S, W, H, D), device="cuda", generator=gen) < outlier_p,
+                               8.0, 1.0))
+            v.mul_(torch.where(torch.rand((S, W, H, D), device="cuda", generator=gen) < outlier_p,
+                               8.0, 1.0))
+        for s in range(S):
+            ring.write(layer, s, int(pos_host[s]) - W + 1, k[s], v[s], stream=stream)
+        del k, v
+    torch.cuda.synchronize()
+
+
+def time_steps(torch, step, steps, warmup, per_launch_events):
+    """Runs warmup steps, then times exactly `steps` steps between two
+    synchronizations.  step(ev) launches one step; when ev is a list it records
+    an event pair around every launch on the launch stream."""
+    for _ in range(warmup):
+        step(None)
+    torch.cuda.synchronize()
+    pairs = [] if per_launch_events else None
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record()
+    for _ in range(steps):
+        step(pairs)
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1)
+    launch_ms = None
+    if pairs:
+        launch_ms = float(np.mean([a.elapsed_time(b) for a, b in pairs]))
+    return ms, launch_ms
+
+
+def bench_b1(torch, iters=200):
+    """BASELINE config 1 at B=1: per-launch time of one layer, from a HIP graph
+    of `iters` back-to-back launches (what a captured decode step replays) and
+    from an eager loop (Python launch cost included)."""
+    from bmo_jetson_amd import KVRing
+
+    H, D, W, P = 32, 128, 512, 700
+    ring = KVRing(1, 1, H, D, W)
+    pos_host = np.array([P], np.int64)
+    fill_ring(torch, ring, 1, 1, H, D, W, pos_host, 0xB0A00001, outlier_p=0.0)
+    stream = torch.cuda.current_stream()
+    pos = torch.tensor([P], dtype=torch.int32, device="cuda")
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0xB0A00001)
+    q = torch.randn(H * D, device="cuda", generator=g)
+    k = torch.randn(H * D, device="cuda", generator=g)
+    v = torch.randn(H * D, device="cuda", generator=g)
+    out = torch.empty(H * D, device="cuda")
+    res = {}
+    for name, fn in (
+        ("fused", lambda: ring.append_decode(0, pos, q, k, v, out, H, stream=stream)),
+        ("decode", lambda: ring.decode(0, pos, q, out, H, stream=stream)),
+    ):
+        for _ in range(20):
+            fn()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(iters):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        eager_us = e0.elapsed_time(e1) * 1000.0 / iters
+        graph = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            stream_cap = torch.cuda.current_stream()
+            with torch.cuda.graph(graph, stream=s):
+                for _ in range(iters):
+                    if name == "fused":
+                        ring.append_decode(0, pos, q, k, v, out, H, stream=stream_cap)
+                    else:
+                        ring.decode(0, pos, q, out, H, stream=stream_cap)
+        torch.cuda.current_stream().wait_stream(s)
+        graph.replay()
+        torch.cuda.synchronize()
+        reps = 5
+        e0.record()
+        for _ in range(reps):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        graph_us = e0.elapsed_time(e1) * 1000.0 / (reps * iters)
+        res[name] = {"graph_us": round(graph_us, 3), "eager_us": round(eager_us, 3)}
+        del graph
+    ring.close()
+    b = unit_bytes(H, D, W)
+    return {
+        "workload": "cfg1: S=1 L=1 H=32 D=128 W=512 pos=700",
+        "us_per_layer_fused_graph": res["fused"]["graph_us"],
+        "us_per_layer_fused_eager": res["fused"]["eager_us"],
+        "us_per_layer_decode_graph": res["decode"]["graph_us"],
+        "us_per_layer_decode_eager": res["decode"]["eager_us"],
+        "decode_GBps_graph": round(b / (res["decode"]["graph_us"] * 1e-6) / 1e9, 1),
+        "target_us": 10.0,
+    }
+
+
+def cpu_baseline(torch, ring, L, S, H, D, W, pos_host, q_dev, out_dev, budget_s):
+    """Times the oracle's fp32 restatement of the reference CPU path
+    (src/bmo_compute.cpp:927-970) on host threads over a sample of the same
+    ring (layer 0, the first n sessions), and checks its output against the GPU
+    output of those sessions."""
+    import oracle
+
+    n_threads = max(1, min(16, len(os.sched_getaffinity(0))))
+
+    def stripes(n):
+        kc = np.zeros((n, H, W, D // 32), dtype=oracle.BLOCK_DTYPE)
+        vc = np.zeros_like(kc)
+        for s in range(n):
+            for which, dst in ((0, kc), (1, vc)):
+                raw = ring.export_q4_0(0, s, which, 0, W)  # [W][H][nblk][18]
+                dst[s] = np.ascontiguousarray(raw.transpose(1, 0, 2, 3)).view(oracle.BLOCK_DTYPE)[..., 0]
+        return kc, vc
+
+    q_host = q_dev[0].float().cpu().numpy()  # layer 0: [S][H][D]
+    kc1, vc1 = stripes(1)
+    secs1, _ = oracle.cpu_baseline_run(kc1, vc1, pos_host[:1], q_host[:1], H, 1, 1)
+    # size the multi-thread sample to ~budget_s
+    per_unit_mt = max(secs1 / max(1, n_threads * 0.8), 1e-4)
+    n_sess = int(min(S, max(n_threads, round(budget_s / per_unit_mt))))
+    iters = max(1, int(budget_s / (per_unit_mt * n_sess)))
+    kc, vc = stripes(n_sess)
+    secs, out = oracle.cpu_baseline_run(kc, vc, pos_host[:n_sess], q_host[:n_sess], H, n_threads,
+                                        iters)
+    secs_1t, _ = oracle.cpu_baseline_run(kc[:1], vc[:1], pos_host[:1], q_host[:1], H, 1, 3)
+    gpu_out = out_dev[0][:n_sess].float().cpu().numpy()
+    max_abs = float(np.max(np.abs(gpu_out - out)))
+    bytes_mt = unit_bytes(H, D, W) * n_sess * iters
+    return {
+        "value": round(bytes_mt / secs / 1e9, 3),
+        "unit": "GB/s",
+        "cores": n_threads,
+        "kind": "port",
+        "sample": f"layer 0 of the cfg3 ring, {n_sess} sessions x {H} heads x W={W}, "
+                  f"{iters} pass(es), {n_threads} threads, {secs:.1f} s",
+        "single_thread_GBps": round(unit_bytes(H, D, W) * 3 / secs_1t / 1e9, 3),
+        "single_thread_us_per_layer_b1": round(secs_1t / 3 * 1e6, 1),
+        "max_abs_vs_gpu": max_abs,
+        "what": "oracle fp32 restatement of the reference CPU decode attention "
+                "(src/bmo_compute.cpp:927-970) over the Q4_0 ring; ggml itself is not available",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="cfg3", choices=["cfg3", "cfg4"])
+    ap.add_argument("--sessions", type=int, default=None, help="override S (testing)")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-b1", action="store_true")
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="only run a plain device copy of this size (rocprof PMC calibration)")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this path runs on one GPU: sessions shard across GPUs with no "
+                          "exchange, so the figure is the one-GPU number; --gpus N>1 is not "
+                          "supported"}))
+        sys.exit(2)
+
+    import torch
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    torch.cuda.init()
+
+    if args.copy_calibration_mib:
+        n = args.copy_calibration_mib * (1 << 20) // 4
+        a = torch.ones(n, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(5):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read": n * 4, "copy_bytes_written": n * 4}))
+        return
+
+    from bmo_jetson_amd import KVRing
+
+    H, D, W, L = 32, 128, 512, 32
+    S = args.sessions or (64 if args.config == "cfg3" else 256)
+    fused = args.config == "cfg4"
+    seed = 0xB0A00003 if args.config == "cfg3" else 0xB0A00004
+    rng = np.random.default_rng(seed)
+    pos_host = rng.integers(512, 4096, size=S).astype(np.int64)
+    log(f"[bench] {args.config}: S={S} L={L} H={H} D={D} W={W} fused={fused}; filling ring")
+    t_fill = time.time()
+    ring = KVRing(L, S, H, D, W)
+    # cfg4 appends the token at pos, so the ring holds the window before it
+    fill_ring(torch, ring, L, S, H, D, W, pos_host - (1 if fused else 0), seed)
+    log(f"[bench] ring {ring.nbytes / 1e9:.2f} GB filled in {time.time() - t_fill:.1f} s")
+
+    stream = torch.cuda.current_stream()
+    pos = torch.tensor(pos_host, dtype=torch.int32, device="cuda")
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed + 7)
+    q = torch.randn((L, S, H, D), device="cuda", generator=g)
+    out = torch.empty((L, S, H, D), device="cuda")
+    if fused:
+        kn = torch.randn((L, S, H, D), device="cuda", generator=g)
+        vn = torch.randn((L, S, H, D), device="cuda", generator=g)
+
+    def step(pairs):
+        for layer in range(L):
+            if pairs is not None:
+                a = torch.cuda.Event(enable_timing=True)
+                b = torch.cuda.Event(enable_timing=True)
+                a.record(stream)
+            if fused:
+                ring.append_decode(layer, pos, q[layer], kn[layer], vn[layer], out[layer], H,
+                                   stream=stream)
+            else:
+                ring.decode(layer, pos, q[layer], out[layer], H, stream=stream)
+            if pairs is not None:
+                b.record(stream)
+                pairs.append((a, b))
+
+    ms, launch_ms = time_steps(torch, step, args.steps, args.warmup, per_launch_events=True)
+    ms_per_step = ms / args.steps
+    per_step_bytes = unit_bytes(H, D, W) * S * L
+    if fused:
+        per_step_bytes += fused_extra_bytes(H, D) * S * L
+    value = per_step_bytes / (ms_per_step * 1e-3) / 1e9
+    launch_bytes = per_step_bytes / L
+    achieved = launch_bytes / (launch_ms * 1e-3) / 1e9
+    log(f"[bench] {ms_per_step:.3f} ms/step, {value:.1f} GB/s; per launch {launch_ms * 1e3:.2f} us "
+        f"-> {achieved:.1f} GB/s")
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": (f"{args.config}: Q4_0 ring {'fused append+' if fused else ''}decode "
+                         f"attention, S={S} sessions x L={L} layers, H={H} x D={D}, W={W}, "
+                         f"pos~U[512,4096), 1% x8 outliers"),
+            "sessions": S, "layers": L, "heads": H, "head_dim": D, "window": W,
+            "bytes_per_step": per_step_bytes, "launches_per_step": L,
+            "parallelism": "none (1 GPU; sessions would shard across GPUs)",
+        },
+        "hbm_frac": round(value / HBM_PEAK_GBS, 4),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "decode_kernel<128, %s>" % ("true" if fused else "false"),
+            "launch_us": round(launch_ms * 1e3, 3),
+            "bytes_per_launch": launch_bytes,
+        },
+    }
+
+    if not args.no_b1:
+        result["b1"] = bench_b1(torch)
+        log(f"[bench] B=1: {result['b1']}")
+    if not args.no_cpu:
+        log("[bench] timing the CPU baseline")
+        result["cpu_baseline"] = cpu_baseline(torch, ring, L, S, H, D, W, pos_host, q, out,
+                                              args.cpu_seconds)
+    ring.close()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,540 @@
+// api.cpp -- the C ABI of include/bmo_attn.h: ring allocation, argument
+// checking, error reporting, readout/export, and the node-level drop-in for
+// the reference's launch_decode_attention.
+//
+// Error behaviour mirrors src/bmo_api.cpp: nothing throws across the ABI
+// (every entry point catches), int entry points return a status and record a
+// message retrievable with bmo_kv_ring_last_error, and a failed create
+// returns NULL after printing to stderr (src/bmo_api.cpp:196-205).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <exception>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/bmo_attn.h"
+#include "kernels.hpp"
+
+struct bmo_kv_ring {
+    bmo::RingGeom g{};
+    int device = 0;
+    uint8_t *mem = nullptr;  // K region, V region, split workspace, counters
+    uint8_t *k_base = nullptr;
+    uint8_t *v_base = nullptr;
+    float *partial = nullptr;
+    unsigned *counters = nullptr;
+    std::mutex mu;  // guards last_error
+    std::string last_error;
+};
+
+namespace {
+
+thread_local std::string t_create_error;
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+int fail(bmo_kv_ring_t *r, int code, const std::string &msg) {
+    if (r) {
+        std::lock_guard<std::mutex> lk(r->mu);
+        r->last_error = msg;
+    }
+    return code;
+}
+
+void clear_error(bmo_kv_ring_t *r) {
+    std::lock_guard<std::mutex> lk(r->mu);
+    r->last_error.clear();
+}
+
+// Makes the ring's device current for the duration of a call.
+struct DeviceGuard {
+    int prev = -1;
+    bool switched = false;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) == hipSuccess && prev != dev) {
+            switched = hipSetDevice(dev) == hipSuccess;
+        }
+    }
+    ~DeviceGuard() {
+        if (switched) (void) hipSetDevice(prev);
+    }
+};
+
+int hip_fail(bmo_kv_ring_t *r, hipError_t e, const char *what) {
+    return fail(r, BMO_ATTN_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+int check_layer(bmo_kv_ring_t *r, int layer, const char *fn) {
+    if (layer < 0 || layer >= r->g.n_layers)
+        return fail(r, BMO_ATTN_ERR_ARG, std::string(fn) + ": layer out of range");
+    return BMO_ATTN_OK;
+}
+
+// Window splits per (entry, head): enough workgroups to cover the GPU when
+// the batch is small, never fewer than 4 waves x one iteration of keys per
+// split.  BMO_ATTN_SPLIT overrides (tuning).
+int choose_split(const bmo::RingGeom &g, int units) {
+    static const int forced = [] {
+        const char *e = std::getenv("BMO_ATTN_SPLIT");
+        return e ? std::atoi(e) : 0;
+    }();
+    const int kpi = 64 / (g.head_dim / bmo::kQK);
+    const int min_keys = 4 * kpi;
+    int s = forced > 0 ? forced : std::max(1, 2048 / std::max(1, units));
+    s = std::min(s, std::max(1, g.n_ctx / min_keys));
+    s = std::min(s, bmo::kMaxSplit);
+    while (s > 1 && (int64_t) units * s > bmo::kMaxSplitUnits) --s;
+    return std::max(1, s);
+}
+
+float f16_to_f32_host(uint16_t h) {
+    const uint32_t sign = ((uint32_t) h & 0x8000u) << 16;
+    const uint32_t e = ((uint32_t) h >> 10) & 0x1Fu;
+    const uint32_t m = (uint32_t) h & 0x3FFu;
+    uint32_t x;
+    if (e == 0x1Fu) {
+        x = sign | 0x7F800000u | (m << 13);
+    } else if (e == 0) {
+        float v = std::ldexp((float) m, -24);
+        std::memcpy(&x, &v, 4);
+        x |= sign;
+    } else {
+        x = sign | ((e + 112u) << 23) | (m << 13);
+    }
+    float f;
+    std::memcpy(&f, &x, 4);
+    return f;
+}
+
+// Copies the nibble and scale rows of slots [t0, t0+n) of one stripe to host.
+hipError_t fetch_rows(const bmo_kv_ring_t *r, const uint8_t *stripe, int t0, int n,
+                      std::vector<uint8_t> &nib, std::vector<uint16_t> &scl) {
+    const int D = r->g.head_dim;
+    nib.resize((size_t) n * D / 2);
+    scl.resize((size_t) n * (D / bmo::kQK));
+    hipError_t e = hipMemcpy(nib.data(), stripe + (int64_t) t0 * D / 2, nib.size(), hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return e;
+    return hipMemcpy(scl.data(), stripe + r->g.nib_bytes + (int64_t) t0 * (D / bmo::kQK) * 2,
+                     scl.size() * 2, hipMemcpyDeviceToHost);
+}
+
+__global__ void zero_ranges_kernel(uint8_t *base, int64_t range_bytes, int64_t range_stride,
+                                   int64_t v_offset) {
+    // blockIdx.y selects (region, range); ranges are 16-byte multiples.
+    const int64_t range = blockIdx.y >> 1;
+    uint8_t *start = base + range * range_stride + ((blockIdx.y & 1) ? v_offset : 0);
+    uint4 *p = reinterpret_cast<uint4 *>(start);
+    const int64_t n = range_bytes / 16;
+    for (int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t) gridDim.x * blockDim.x)
+        p[i] = make_uint4(0, 0, 0, 0);
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t bmo_kv_ring_stripe_bytes(int head_dim, int n_ctx) {
+    if (head_dim <= 0 || n_ctx <= 0) return 0;
+    return bmo::stripe_bytes_for(head_dim, n_ctx);
+}
+
+bmo_kv_ring_t *bmo_kv_ring_create(int n_layers, int n_sessions, int n_kv_heads, int head_dim,
+                                  int n_ctx) {
+    t_create_error.clear();
+    auto reject = [](const std::string &m) -> bmo_kv_ring_t * {
+        t_create_error = "bmo_kv_ring_create: " + m;
+        std::fprintf(stderr, "[bmo_attn] %s\n", t_create_error.c_str());
+        return nullptr;
+    };
+    if (n_layers <= 0 || n_sessions <= 0 || n_kv_heads <= 0)
+        return reject("n_layers, n_sessions and n_kv_heads must be positive");
+    if (head_dim != 64 && head_dim != 128) return reject("head_dim must be 64 or 128");
+    if (n_ctx <= 0 || n_ctx > 65536) return reject("n_ctx must be in [1, 65536]");
+    try {
+        auto *r = new bmo_kv_ring();
+        r->g = bmo::make_geom(n_layers, n_sessions, n_kv_heads, head_dim, n_ctx);
+        if (hipGetDevice(&r->device) != hipSuccess) {
+            delete r;
+            return reject("no HIP device");
+        }
+        const int64_t region = r->g.region_bytes();
+        const int64_t part_bytes = (int64_t) bmo::kMaxSplitUnits * (head_dim + 2) * 4;
+        const int64_t cnt_bytes = (int64_t) bmo::kMaxSplitUnits * 4;
+        const int64_t total = 2 * region + part_bytes + cnt_bytes;
+        hipError_t e = hipMalloc(&r->mem, (size_t) total);
+        if (e != hipSuccess) {
+            delete r;
+            return reject(std::string("hipMalloc of ") + std::to_string(total) +
+                          " bytes failed: " + hipGetErrorString(e));
+        }
+        e = hipMemset(r->mem, 0, (size_t) total);
+        if (e == hipSuccess) e = hipDeviceSynchronize();
+        if (e != hipSuccess) {
+            (void) hipFree(r->mem);
+            delete r;
+            return reject(std::string("hipMemset failed: ") + hipGetErrorString(e));
+        }
+        r->k_base = r->mem;
+        r->v_base = r->mem + region;
+        r->partial = reinterpret_cast<float *>(r->mem + 2 * region);
+        r->counters = reinterpret_cast<unsigned *>(r->mem + 2 * region + part_bytes);
+        return r;
+    } catch (const std::exception &ex) {
+        return reject(ex.what());
+    } catch (...) {
+        return reject("unknown exception");
+    }
+}
+
+void bmo_kv_ring_free(bmo_kv_ring_t *ring) {
+    if (!ring) return;
+    try {
+        DeviceGuard dg(ring->device);
+        if (ring->mem) (void) hipFree(ring->mem);
+    } catch (...) {
+    }
+    delete ring;
+}
+
+int bmo_kv_ring_geometry(const bmo_kv_ring_t *r, int *n_layers, int *n_sessions, int *n_kv_heads,
+                         int *head_dim, int *n_ctx) {
+    if (!r) return BMO_ATTN_ERR_NULL;
+    if (n_layers) *n_layers = r->g.n_layers;
+    if (n_sessions) *n_sessions = r->g.n_sessions;
+    if (n_kv_heads) *n_kv_heads = r->g.n_kv_heads;
+    if (head_dim) *head_dim = r->g.head_dim;
+    if (n_ctx) *n_ctx = r->g.n_ctx;
+    return BMO_ATTN_OK;
+}
+
+int64_t bmo_kv_ring_bytes(const bmo_kv_ring_t *r) { return r ? 2 * r->g.region_bytes() : 0; }
+
+void *bmo_kv_ring_k_base(bmo_kv_ring_t *r) { return r ? r->k_base : nullptr; }
+void *bmo_kv_ring_v_base(bmo_kv_ring_t *r) { return r ? r->v_base : nullptr; }
+
+const char *bmo_kv_ring_last_error(const bmo_kv_ring_t *r) {
+    if (!r) return t_create_error.empty() ? nullptr : t_create_error.c_str();
+    auto *m = const_cast<bmo_kv_ring_t *>(r);
+    std::lock_guard<std::mutex> lk(m->mu);
+    return m->last_error.empty() ? nullptr : m->last_error.c_str();
+}
+
+int bmo_kv_ring_reset(bmo_kv_ring_t *r, int session, void *stream) {
+    if (!r) return BMO_ATTN_ERR_NULL;
+    try {
+        if (session < -1 || session >= r->g.n_sessions)
+            return fail(r, BMO_ATTN_ERR_ARG, "bmo_kv_ring_reset: session out of range");
+        DeviceGuard dg(r->device);
+        const bmo::RingGeom &g = r->g;
+        int64_t range_bytes, stride;
+        unsigned n_ranges;
+        uint8_t *base;
+        if (session == -1) {
+            base = r->k_base;
+            range_bytes = g.region_bytes();
+            stride = 0;
+            n_ranges = 1;
+        } else {
+            // session s of layer l: n_kv_heads contiguous stripes
+            base = r->k_base + g.stripe_offset(0, session, 0);
+            range_bytes = (int64_t) g.n_kv_heads * g.stripe_bytes;
+            stride = (int64_t) g.n_sessions * g.n_kv_heads * g.stripe_bytes;
+            n_ranges = (unsigned) g.n_layers;
+        }
+        const int64_t vecs = range_bytes / 16;
+        const unsigned gx = (unsigned) std::min<int64_t>((vecs + 255) / 256, 4096);
+        hipLaunchKernelGGL(zero_ranges_kernel, dim3(gx, 2 * n_ranges), dim3(256), 0,
+                           (hipStream_t) stream, base, range_bytes, stride, g.region_bytes());
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return hip_fail(r, e, "bmo_kv_ring_reset");
+        clear_error(r);
+        return BMO_ATTN_OK;
+    } catch (...) {
+        return fail(r, BMO_ATTN_ERR_INTERNAL, "bmo_kv_ring_reset: unknown exception");
+    }
+}
+
+int bmo_kv_ring_append(bmo_kv_ring_t *r, int layer, int n_batch, const int *session_ids,
+                       const int *pos, const float *k_new, const float *v_new, void *stream) {
+    if (!r) return BMO_ATTN_ERR_NULL;
+    try {
+        if (!pos || !k_new || !v_new)
+            return fail(r, BMO_ATTN_ERR_NULL, "bmo_kv_ring_append: null pointer argument");
+        if (int rc = check_layer(r, layer, "bmo_kv_ring_append")) return rc;
+        if (n_batch <= 0 || n_batch > r->g.n_sessions)
+            return fail(r, BMO_ATTN_ERR_ARG, "bmo_kv_ring_append: n_batch must be in [1, n_sessions]");
+        DeviceGuard dg(r->device);
+        bmo::AppendParams p{};
+        p.k_base = r->k_base;
+        p.v_base = r->v_base;
+        p.g = r->g;
+        p.layer = layer;
+        p.n_rows = n_batch;
+        p.session_ids = session_ids;
+        p.pos = pos;
+        p.k = k_new;
+        p.v = v_new;
+        bmo::launch_append(p, (hipStream_t) stream);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return hip_fail(r, e, "bmo_kv_ring_append");
+        clear_error(r);
+        return BMO_ATTN_OK;
+    } catch (...) {
+        return fail(r, BMO_ATTN_ERR_INTERNAL, "bmo_kv_ring_append: unknown exception");
+    }
+}
+
+static int decode_common(bmo_kv_ring_t *r, const char *fn, bool fused, int layer, int n_batch,
+                         const int *session_ids, const int *pos, int n_heads, const float *q,
+                         const float *k_new, const float *v_new, float *out, float scale,
+                         void *stream) {
+    if (!r) return BMO_ATTN_ERR_NULL;
+    try {
+        if (!pos || !q || !out || (fused && (!k_new || !v_new)))
+            return fail(r, BMO_ATTN_ERR_NULL, std::string(fn) + ": null pointer argument");
+        if (int rc = check_layer(r, layer, fn)) return rc;
+        if (n_batch <= 0 || n_batch > r->g.n_sessions)
+            return fail(r, BMO_ATTN_ERR_ARG, std::string(fn) + ": n_batch must be in [1, n_sessions]");
+        if (n_heads <= 0 || n_heads % r->g.n_kv_heads != 0)
+            return fail(r, BMO_ATTN_ERR_ARG,
+                        std::string(fn) + ": n_heads must be a positive multiple of n_kv_heads");
+        if (!(scale > 0.0f)) scale = 1.0f / std::sqrt((float) r->g.head_dim);
+        if (!std::isfinite(scale))
+            return fail(r, BMO_ATTN_ERR_ARG, std::string(fn) + ": scale must be finite");
+        DeviceGuard dg(r->device);
+        bmo::DecodeParams p{};
+        p.k_base = r->k_base;
+        p.v_base = r->v_base;
+        p.k_wbase = r->k_base;
+        p.v_wbase = r->v_base;
+        p.g = r->g;
+        p.layer = layer;
+        p.n_batch = n_batch;
+        p.n_heads = n_heads;
+        p.n_kv = r->g.n_kv_heads;
+        p.n_split = choose_split(r->g, n_batch * n_heads);
+        p.session_ids = session_ids;
+        p.pos = pos;
+        p.q = q;
+        p.k_new = k_new;
+        p.v_new = v_new;
+        p.out = out;
+        p.qscale = scale * kLog2e;
+        p.partial = r->partial;
+        p.counters = r->counters;
+        if (!bmo::launch_decode(p, fused, (hipStream_t) stream))
+            return fail(r, BMO_ATTN_ERR_ARG, std::string(fn) + ": unsupported head_dim");
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return hip_fail(r, e, fn);
+        clear_error(r);
+        return BMO_ATTN_OK;
+    } catch (...) {
+        return fail(r, BMO_ATTN_ERR_INTERNAL, std::string(fn) + ": unknown exception");
+    }
+}
+
+int bmo_kv_ring_decode(bmo_kv_ring_t *r, int layer, int n_batch, const int *session_ids,
+                       const int *pos, int n_heads, const float *q, float *out, float scale,
+                       void *stream) {
+    return decode_common(r, "bmo_kv_ring_decode", false, layer, n_batch, session_ids, pos, n_heads,
+                         q, nullptr, nullptr, out, scale, stream);
+}
+
+int bmo_kv_ring_append_decode(bmo_kv_ring_t *r, int layer, int n_batch, const int *session_ids,
+                              const int *pos, int n_heads, const float *q, const float *k_new,
+                              const float *v_new, float *out, float scale, void *stream) {
+    return decode_common(r, "bmo_kv_ring_append_decode", true, layer, n_batch, session_ids, pos,
+                         n_heads, q, k_new, v_new, out, scale, stream);
+}
+
+int bmo_kv_ring_write(bmo_kv_ring_t *r, int layer, int session, int64_t pos0, int n_tok,
+                      const float *k, const float *v, void *stream) {
+    if (!r) return BMO_ATTN_ERR_NULL;
+    try {
+        if (!k || !v) return fail(r, BMO_ATTN_ERR_NULL, "bmo_kv_ring_write: null pointer argument");
+        if (int rc = check_layer(r, layer, "bmo_kv_ring_write")) return rc;
+        if (session < 0 || session >= r->g.n_sessions)
+            return fail(r, BMO_ATTN_ERR_ARG, "bmo_kv_ring_write: session out of range");
+        if (pos0 < 0) return fail(r, BMO_ATTN_ERR_ARG, "bmo_kv_ring_write: pos0 must be >= 0");
+        if (n_tok <= 0 || n_tok > r->g.n_ctx)
+            return fail(r, BMO_ATTN_ERR_ARG, "bmo_kv_ring_write: n_tok must be in [1, n_ctx]");
+        DeviceGuard dg(r->device);
+        bmo::AppendParams p{};
+        p.k_base = r->k_base;
+        p.v_base = r->v_base;
+        p.g = r->g;
+        p.layer = layer;
+        p.n_rows = n_tok;
+        p.session = session;
+        p.pos0 = pos0;
+        p.k = k;
+        p.v = v;
+        bmo::launch_append(p, (hipStream_t) stream);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return hip_fail(r, e, "bmo_kv_ring_write");
+        clear_error(r);
+        return BMO_ATTN_OK;
+    } catch (...) {
+        return fail(r, BMO_ATTN_ERR_INTERNAL, "bmo_kv_ring_write: unknown exception");
+    }
+}
+
+int bmo_kv_ring_copy_k_f32(bmo_kv_ring_t *r, int layer, int session, int t_start, int n_positions,
+                           float *out, int max_floats) {
+    if (!r || !out || n_positions <= 0 || max_floats <= 0) return BMO_ATTN_READ_ERR_NULL;
+    try {
+        const bmo::RingGeom &g = r->g;
+        if (session < 0 || session >= g.n_sessions) return BMO_ATTN_READ_ERR_NULL;
+        if (layer < 0 || layer >= g.n_layers) return BMO_ATTN_READ_ERR_RANGE;
+        if (t_start < 0 || (int64_t) t_start + n_positions > g.n_ctx) return BMO_ATTN_READ_ERR_RANGE;
+        const int64_t need = (int64_t) n_positions * g.n_kv_heads * g.head_dim;
+        if (need > (int64_t) max_floats) return BMO_ATTN_READ_ERR_SMALL;
+        DeviceGuard dg(r->device);
+        if (hipDeviceSynchronize() != hipSuccess) return BMO_ATTN_READ_ERR_NULL;
+        const int D = g.head_dim;
+        const int nblk = D / bmo::kQK;
+        std::vector<uint8_t> nib;
+        std::vector<uint16_t> scl;
+        for (int h = 0; h < g.n_kv_heads; ++h) {
+            const uint8_t *stripe = r->k_base + g.stripe_offset(layer, session, h);
+            if (fetch_rows(r, stripe, t_start, n_positions, nib, scl) != hipSuccess)
+                return BMO_ATTN_READ_ERR_NULL;
+            for (int ti = 0; ti < n_positions; ++ti) {
+                float *o = out + ((int64_t) ti * g.n_kv_heads + h) * D;
+                for (int b = 0; b < nblk; ++b) {
+                    const float d = f16_to_f32_host(scl[(size_t) ti * nblk + b]);
+                    const uint8_t *qs = nib.data() + (size_t) ti * D / 2 + b * 16;
+                    for (int j = 0; j < 16; ++j) {
+                        o[b * 32 + j] = (float) ((int) (qs[j] & 0x0F) - 8) * d;
+                        o[b * 32 + j + 16] = (float) ((int) (qs[j] >> 4) - 8) * d;
+                    }
+                }
+            }
+        }
+        return (int) need;
+    } catch (...) {
+        return BMO_ATTN_READ_ERR_NULL;
+    }
+}
+
+int64_t bmo_kv_ring_export_q4_0(bmo_kv_ring_t *r, int layer, int session, int which, int t_start,
+                                int n_positions, void *out, int64_t max_bytes) {
+    if (!r || !out || n_positions <= 0 || max_bytes <= 0) return BMO_ATTN_READ_ERR_NULL;
+    try {
+        const bmo::RingGeom &g = r->g;
+        if (session < 0 || session >= g.n_sessions || (which != 0 && which != 1))
+            return BMO_ATTN_READ_ERR_NULL;
+        if (layer < 0 || layer >= g.n_layers) return BMO_ATTN_READ_ERR_RANGE;
+        if (t_start < 0 || (int64_t) t_start + n_positions > g.n_ctx) return BMO_ATTN_READ_ERR_RANGE;
+        const int nblk = g.head_dim / bmo::kQK;
+        const int64_t need = (int64_t) n_positions * g.n_kv_heads * nblk * 18;
+        if (need > max_bytes) return BMO_ATTN_READ_ERR_SMALL;
+        DeviceGuard dg(r->device);
+        if (hipDeviceSynchronize() != hipSuccess) return BMO_ATTN_READ_ERR_NULL;
+        uint8_t *dst = static_cast<uint8_t *>(out);
+        std::vector<uint8_t> nib;
+        std::vector<uint16_t> scl;
+        const uint8_t *base = which == 0 ? r->k_base : r->v_base;
+        for (int h = 0; h < g.n_kv_heads; ++h) {
+            if (fetch_rows(r, base + g.stripe_offset(layer, session, h), t_start, n_positions, nib,
+                           scl) != hipSuccess)
+                return BMO_ATTN_READ_ERR_NULL;
+            for (int ti = 0; ti < n_positions; ++ti)
+                for (int b = 0; b < nblk; ++b) {
+                    uint8_t *blkp = dst + (((int64_t) ti * g.n_kv_heads + h) * nblk + b) * 18;
+                    std::memcpy(blkp, &scl[(size_t) ti * nblk + b], 2);
+                    std::memcpy(blkp + 2, nib.data() + (size_t) ti * g.head_dim / 2 + b * 16, 16);
+                }
+        }
+        return need;
+    } catch (...) {
+        return BMO_ATTN_READ_ERR_NULL;
+    }
+}
+
+int64_t bmo_kv_ring_import_q4_0(bmo_kv_ring_t *r, int layer, int session, int which, int t_start,
+                                int n_positions, const void *in, int64_t n_bytes) {
+    if (!r || !in || n_positions <= 0 || n_bytes <= 0) return BMO_ATTN_READ_ERR_NULL;
+    try {
+        const bmo::RingGeom &g = r->g;
+        if (session < 0 || session >= g.n_sessions || (which != 0 && which != 1))
+            return BMO_ATTN_READ_ERR_NULL;
+        if (layer < 0 || layer >= g.n_layers) return BMO_ATTN_READ_ERR_RANGE;
+        if (t_start < 0 || (int64_t) t_start + n_positions > g.n_ctx) return BMO_ATTN_READ_ERR_RANGE;
+        const int nblk = g.head_dim / bmo::kQK;
+        const int64_t need = (int64_t) n_positions * g.n_kv_heads * nblk * 18;
+        if (n_bytes < need) return BMO_ATTN_READ_ERR_SMALL;
+        DeviceGuard dg(r->device);
+        if (hipDeviceSynchronize() != hipSuccess) return BMO_ATTN_READ_ERR_NULL;
+        const uint8_t *src = static_cast<const uint8_t *>(in);
+        std::vector<uint8_t> nib((size_t) n_positions * g.head_dim / 2);
+        std::vector<uint16_t> scl((size_t) n_positions * nblk);
+        uint8_t *base = which == 0 ? r->k_base : r->v_base;
+        for (int h = 0; h < g.n_kv_heads; ++h) {
+            for (int ti = 0; ti < n_positions; ++ti)
+                for (int b = 0; b < nblk; ++b) {
+                    const uint8_t *blkp = src + (((int64_t) ti * g.n_kv_heads + h) * nblk + b) * 18;
+                    std::memcpy(&scl[(size_t) ti * nblk + b], blkp, 2);
+                    std::memcpy(nib.data() + (size_t) ti * g.head_dim / 2 + b * 16, blkp + 2, 16);
+                }
+            uint8_t *stripe = base + g.stripe_offset(layer, session, h);
+            if (hipMemcpy(stripe + (int64_t) t_start * g.head_dim / 2, nib.data(), nib.size(),
+                          hipMemcpyHostToDevice) != hipSuccess ||
+                hipMemcpy(stripe + g.nib_bytes + (int64_t) t_start * nblk * 2, scl.data(),
+                          scl.size() * 2, hipMemcpyHostToDevice) != hipSuccess)
+                return BMO_ATTN_READ_ERR_NULL;
+        }
+        return need;
+    } catch (...) {
+        return BMO_ATTN_READ_ERR_NULL;
+    }
+}
+
+void bmo_launch_decode_attention(const float *q_dev, const float *k_dev, const float *v_dev,
+                                 void *k_cache_dev, void *v_cache_dev, float *out_dev, int head_dim,
+                                 int n_heads, int n_kv_heads, int n_ctx, int n_past, int layer,
+                                 void *stream, const int *pos_dev) {
+    // Mirrors src/bmo_cuda_kernels.cu:850-884: no status is returned, so
+    // rejected arguments launch nothing (as an invalid launch would) and are
+    // reported on stderr once.
+    if (!q_dev || !k_dev || !v_dev || !k_cache_dev || !v_cache_dev || !out_dev ||
+        (head_dim != 64 && head_dim != 128) || n_heads <= 0 || n_kv_heads <= 0 ||
+        n_heads % n_kv_heads != 0 || n_ctx <= 0 || n_ctx > 65536 || layer < 0 ||
+        (pos_dev == nullptr && n_past < 0)) {
+        static bool warned = false;
+        if (!warned) {
+            warned = true;
+            std::fprintf(stderr, "[bmo_attn] bmo_launch_decode_attention: invalid arguments\n");
+        }
+        return;
+    }
+    bmo::DecodeParams p{};
+    // The reference cache has n_heads head slots per layer and one session.
+    p.g = bmo::make_geom(layer + 1, 1, n_heads, head_dim, n_ctx);
+    p.k_base = static_cast<const uint8_t *>(k_cache_dev);
+    p.v_base = static_cast<const uint8_t *>(v_cache_dev);
+    p.k_wbase = static_cast<uint8_t *>(k_cache_dev);
+    p.v_wbase = static_cast<uint8_t *>(v_cache_dev);
+    p.layer = layer;
+    p.n_batch = 1;
+    p.n_heads = n_heads;
+    p.n_kv = n_kv_heads;
+    p.n_split = 1;
+    p.pos = pos_dev;
+    p.pos_scalar = n_past;
+    p.q = q_dev;
+    p.k_new = k_dev;
+    p.v_new = v_dev;
+    p.out = out_dev;
+    p.qscale = (1.0f / std::sqrt((float) head_dim)) * kLog2e;
+    bmo::launch_decode(p, true, (hipStream_t) stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,62 @@
+// append.hip -- quantize fp32 K/V rows into Q4_0 ring slots.
+//
+// The reference writes the current token's K and V as fp16 into slot
+// pos % n_ctx (src/bmo_cuda_kernels.cu:749-754) and, on its multi-token path,
+// copies a chunk into consecutive slots (src/bmo_compute.cpp:2390-2401).  Here
+// the write quantizes to Q4_0, bit-exactly as ggml quantize_row_q4_0_ref.
+//
+// One thread owns one 32-element block: it loads the block's 128 contiguous
+// bytes with eight 128-bit loads, runs the sequential first-occurrence max
+// scan of the reference algorithm in registers, and stores 16 code bytes and
+// a 2-byte scale.  The traffic is 2 * n_kv_heads * head_dim * 4 bytes in per
+// row, so this kernel is small next to the attention read; it is written for
+// exactness, with coalescing left to the cache.
+#include "kernels.hpp"
+#include "q4_0_device.hpp"
+
+namespace bmo {
+
+__global__ __launch_bounds__(256) void append_kernel(AppendParams p) {
+    const int nblk = p.g.head_dim / kQK;
+    const int64_t per_row = (int64_t) p.g.n_kv_heads * nblk * 2;  // blocks of K and V
+    const int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= per_row * p.n_rows) return;
+    const int r = (int) (t / per_row);
+    int rem = (int) (t % per_row);
+    const int which = rem / (p.g.n_kv_heads * nblk);  // 0 = K, 1 = V
+    rem %= p.g.n_kv_heads * nblk;
+    const int h = rem / nblk;
+    const int blk = rem % nblk;
+
+    int session;
+    int64_t pos;
+    if (p.pos != nullptr) {
+        session = p.session_ids ? p.session_ids[r] : r;
+        pos = p.pos[r];
+    } else {
+        session = p.session;
+        pos = p.pos0 + r;
+    }
+    if (session < 0 || session >= p.g.n_sessions || pos < 0) return;
+    const int slot = (int) (pos % p.g.n_ctx);
+
+    const float *src = (which == 0 ? p.k : p.v) +
+                       ((int64_t) r * p.g.n_kv_heads + h) * p.g.head_dim + blk * kQK;
+    float x[kQK];
+    load_block_f32(src, x);
+    uint16_t d16;
+    uint32_t qs[4];
+    quantize_block_q4_0(x, d16, qs);
+    uint8_t *stripe = (which == 0 ? p.k_base : p.v_base) + p.g.stripe_offset(p.layer, session, h);
+    store_block(stripe, p.g, slot, blk, d16, qs);
+}
+
+void launch_append(const AppendParams &p, hipStream_t stream) {
+    const int nblk = p.g.head_dim / kQK;
+    const int64_t threads = (int64_t) p.n_rows * p.g.n_kv_heads * nblk * 2;
+    if (threads <= 0) return;
+    const int64_t grid = (threads + 255) / 256;
+    hipLaunchKernelGGL(append_kernel, dim3((unsigned) grid), dim3(256), 0, stream, p);
+}
+
+}  // namespace bmo

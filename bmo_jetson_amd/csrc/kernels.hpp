@@ -1,0 +1,64 @@
+// kernels.hpp -- parameter blocks and launchers of the ring kernels (internal
+// to libbmo_attn.so; the public surface is include/bmo_attn.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "ring_layout.hpp"
+
+namespace bmo {
+
+// Rows of fp32 K/V to quantize into ring slots.  Row r of the input goes to
+//   batched mode (session_ids/pos set): session session_ids[r] (or r),
+//                                       slot pos[r] % n_ctx;
+//   run mode (pos == nullptr):          session `session`,
+//                                       slot (pos0 + r) % n_ctx.
+struct AppendParams {
+    uint8_t *k_base;
+    uint8_t *v_base;
+    RingGeom g;
+    int layer;
+    int n_rows;
+    const int *session_ids;  // device, nullable (batched mode)
+    const int *pos;          // device (batched mode) or nullptr (run mode)
+    int session;             // run mode
+    int64_t pos0;            // run mode
+    const float *k;          // [n_rows][n_kv_heads][head_dim]
+    const float *v;
+};
+
+struct DecodeParams {
+    const uint8_t *k_base;
+    const uint8_t *v_base;
+    uint8_t *k_wbase;  // fused append target (== k_base)
+    uint8_t *v_wbase;
+    RingGeom g;
+    int layer;
+    int n_batch;
+    int n_heads;
+    int n_kv;                // logical kv heads: GQA map and k_new/v_new row stride
+                             // (g.n_kv_heads is the allocated head count per stripe set)
+    int n_split;             // workgroups per (entry, head); 1 = no merge pass
+    const int *session_ids;  // device, nullable
+    const int *pos;          // device [n_batch], or nullptr -> pos_scalar
+    int pos_scalar;
+    const float *q;      // [n_batch][n_heads][head_dim]
+    const float *k_new;  // [n_batch][n_kv_heads][head_dim] (fused only)
+    const float *v_new;
+    float *out;          // [n_batch][n_heads][head_dim]
+    float qscale;        // softmax scale * log2(e)
+    float *partial;      // [n_batch*n_heads][n_split][head_dim + 2] (n_split > 1)
+    unsigned *counters;  // [n_batch*n_heads], zero between launches (n_split > 1)
+};
+
+// Launchers enqueue only; they leave launch errors for the caller's
+// hipGetLastError().  launch_decode returns false for an unsupported head_dim.
+void launch_append(const AppendParams &p, hipStream_t stream);
+bool launch_decode(const DecodeParams &p, bool fused, hipStream_t stream);
+
+// Largest (entry, head) unit count times n_split the split workspace covers.
+constexpr int kMaxSplitUnits = 16384;
+constexpr int kMaxSplit = 16;
+
+}  // namespace bmo

@@ -1,0 +1,101 @@
+// q4_0_device.hpp -- device-side Q4_0 block quantization, bit-exact with
+// ggml quantize_row_q4_0_ref as compiled for x86-64.
+//
+// Exactness rests on four properties of this build (checked in the ISA and by
+// the parity tests): fp32 division is correctly rounded (hipcc emits the
+// div_scale/div_fmas/div_fixup sequence), fp32 and fp16 denormals are kept
+// (float_denorm_mode 3), the fp32->fp16 conversion rounds to nearest even,
+// and no multiply-add below is contracted into an FMA.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "ring_layout.hpp"
+
+namespace bmo {
+
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float x) {
+    const _Float16 h = (_Float16) x;
+    return __builtin_bit_cast(uint16_t, h);
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t bits) {
+    return (float) __builtin_bit_cast(_Float16, (uint16_t) bits);
+}
+
+// (int8_t)s as an x86-64 compiler evaluates it: a truncating 32-bit
+// conversion that yields 0x80000000 for NaN or out-of-range values, whose low
+// byte is then kept.  Only scales whose reciprocal overflows
+// (|max| < ~2^-125) reach the out-of-range branch.
+__device__ __forceinline__ int x86_trunc_to_i8(float s) {
+    const int i = (__builtin_fabsf(s) < 2147483648.0f) ? (int) s : (int) 0x80000000;
+    return (int) (int8_t) (i & 0xFF);
+}
+
+// Quantizes one 32-element block (ggml quantize_row_q4_0_ref steps):
+//   signed value of largest magnitude, first occurrence, running |max| from
+//   +0.0f; d = max / -8; id = d ? 1/d : 0; scale stored as fp16(d);
+//   code = min(15, (int8_t)(x*id + 8.5f)) with separately rounded multiply
+//   and add.  d16 receives the fp16 scale bits and qs[c] bytes 4c..4c+3 of
+//   the block (byte j = code j | code j+16 << 4).
+__device__ __forceinline__ void quantize_block_q4_0(const float (&x)[kQK], uint16_t &d16,
+                                                    uint32_t (&qs)[4]) {
+#pragma clang fp contract(off)
+    float amax = 0.0f;
+    float vmax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kQK; ++j) {
+        const float a = __builtin_fabsf(x[j]);
+        if (amax < a) {
+            amax = a;
+            vmax = x[j];
+        }
+    }
+    const float d = vmax / -8.0f;
+    const float id = (d != 0.0f) ? 1.0f / d : 0.0f;
+    d16 = f32_to_f16_bits(d);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int j = 4 * c + i;
+            const float p0 = __fmul_rn(x[j], id);
+            const float p1 = __fmul_rn(x[j + 16], id);
+            int c0 = x86_trunc_to_i8(__fadd_rn(p0, 8.5f));
+            int c1 = x86_trunc_to_i8(__fadd_rn(p1, 8.5f));
+            c0 = c0 > 15 ? 15 : c0;
+            c1 = c1 > 15 ? 15 : c1;
+            const uint32_t byte = ((uint32_t) c0 | ((uint32_t) c1 << 4)) & 0xFFu;
+            w |= byte << (8 * i);
+        }
+        qs[c] = w;
+    }
+}
+
+// Loads one block's 32 fp32 elements (16-byte aligned source).
+__device__ __forceinline__ void load_block_f32(const float *__restrict__ src, float (&x)[kQK]) {
+    const float4 *s4 = reinterpret_cast<const float4 *>(src);
+#pragma unroll
+    for (int c = 0; c < kQK / 4; ++c) {
+        const float4 t = s4[c];
+        x[4 * c + 0] = t.x;
+        x[4 * c + 1] = t.y;
+        x[4 * c + 2] = t.z;
+        x[4 * c + 3] = t.w;
+    }
+}
+
+// Stores a quantized block at slot `slot`, block `blk` of a ring stripe.
+__device__ __forceinline__ void store_block(uint8_t *__restrict__ stripe, const RingGeom &g,
+                                            int slot, int blk, uint16_t d16,
+                                            const uint32_t (&qs)[4]) {
+    uint4 *nib = reinterpret_cast<uint4 *>(stripe + (int64_t) slot * (g.head_dim / 2) + blk * 16);
+    *nib = make_uint4(qs[0], qs[1], qs[2], qs[3]);
+    uint16_t *sc = reinterpret_cast<uint16_t *>(stripe + g.nib_bytes +
+                                                ((int64_t) slot * (g.head_dim / kQK) + blk) * 2);
+    *sc = d16;
+}
+
+}  // namespace bmo

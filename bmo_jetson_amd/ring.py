@@ -1,0 +1,207 @@
+"""Python view of the Q4_0 ring (ctypes over include/bmo_attn.h).
+
+Mirrors the KV-touching part of the reference's Python binding
+(``bmo_engine.py``): ``reset`` (bmo_engine.py:135-137) and
+``get_k_cache_f32`` (bmo_engine.py:258-280, same layout
+``(n_positions, n_heads, head_dim)`` and the same errors), plus the batched
+append / decode entry points that the reference's single-session handle does
+not have.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from ._lib import lib
+
+BLOCK_Q4_0_BYTES = 18
+
+
+class RingError(RuntimeError):
+    def __init__(self, fn: str, rc: int, msg: str | None):
+        super().__init__(f"{fn} rc={rc}: {msg or 'unknown'}")
+        self.rc = rc
+
+
+def _ptr(x) -> int | None:
+    """Device (or host) address of a tensor / int / None."""
+    if x is None:
+        return None
+    if isinstance(x, int):
+        return x
+    if hasattr(x, "data_ptr"):
+        return int(x.data_ptr())
+    raise TypeError(f"expected a tensor, an int address or None, got {type(x)!r}")
+
+
+def _stream(s) -> int | None:
+    if s is None:
+        return None
+    if isinstance(s, int):
+        return s
+    if hasattr(s, "cuda_stream"):
+        return int(s.cuda_stream)
+    raise TypeError(f"expected a stream, an int handle or None, got {type(s)!r}")
+
+
+def stripe_bytes(head_dim: int, n_ctx: int) -> int:
+    return int(lib().bmo_kv_ring_stripe_bytes(head_dim, n_ctx))
+
+
+class KVRing:
+    """A device-resident Q4_0 ring: [n_layers][n_sessions][n_kv_heads] stripes
+    of n_ctx slots.  The reference's temporal cache is
+    ``KVRing(32, 1, 32, 128, 512)``, its depformer cache ``KVRing(6, 1, 16, 64, 8)``.
+    """
+
+    def __init__(self, n_layers: int, n_sessions: int, n_kv_heads: int, head_dim: int,
+                 n_ctx: int):
+        L = lib()
+        h = L.bmo_kv_ring_create(n_layers, n_sessions, n_kv_heads, head_dim, n_ctx)
+        if not h:
+            err = L.bmo_kv_ring_last_error(None)
+            raise RuntimeError(f"bmo_kv_ring_create failed: {err.decode() if err else 'unknown'}")
+        self._h = h
+        self.n_layers = n_layers
+        self.n_sessions = n_sessions
+        self.n_kv_heads = n_kv_heads
+        self.head_dim = head_dim
+        self.n_ctx = n_ctx
+
+    # -- lifetime ---------------------------------------------------------------
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            lib().bmo_kv_ring_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    @property
+    def handle(self) -> int:
+        return self._h
+
+    @property
+    def nbytes(self) -> int:
+        return int(lib().bmo_kv_ring_bytes(self._h))
+
+    @property
+    def k_base(self) -> int:
+        return int(lib().bmo_kv_ring_k_base(self._h))
+
+    @property
+    def v_base(self) -> int:
+        return int(lib().bmo_kv_ring_v_base(self._h))
+
+    def geometry(self):
+        vals = [ctypes.c_int() for _ in range(5)]
+        rc = lib().bmo_kv_ring_geometry(self._h, *[ctypes.byref(v) for v in vals])
+        self._check("bmo_kv_ring_geometry", rc)
+        return tuple(v.value for v in vals)
+
+    def last_error(self) -> str | None:
+        e = lib().bmo_kv_ring_last_error(self._h)
+        return e.decode() if e else None
+
+    def _check(self, fn: str, rc: int) -> None:
+        if rc != 0:
+            raise RingError(fn, rc, self.last_error())
+
+    # -- state ------------------------------------------------------------------
+    def reset(self, session: int = -1, stream=None) -> None:
+        self._check("bmo_kv_ring_reset",
+                    lib().bmo_kv_ring_reset(self._h, session, _stream(stream)))
+
+    # -- decode path ------------------------------------------------------------
+    def append(self, layer: int, pos, k, v, session_ids=None, n_batch=None, stream=None):
+        n = self._batch(pos, n_batch)
+        self._check("bmo_kv_ring_append", lib().bmo_kv_ring_append(
+            self._h, layer, n, _ptr(session_ids), _ptr(pos), _ptr(k), _ptr(v), _stream(stream)))
+
+    def decode(self, layer: int, pos, q, out, n_heads: int, session_ids=None, scale: float = 0.0,
+               n_batch=None, stream=None):
+        n = self._batch(pos, n_batch)
+        self._check("bmo_kv_ring_decode", lib().bmo_kv_ring_decode(
+            self._h, layer, n, _ptr(session_ids), _ptr(pos), n_heads, _ptr(q), _ptr(out),
+            float(scale), _stream(stream)))
+
+    def append_decode(self, layer: int, pos, q, k, v, out, n_heads: int, session_ids=None,
+                      scale: float = 0.0, n_batch=None, stream=None):
+        n = self._batch(pos, n_batch)
+        self._check("bmo_kv_ring_append_decode", lib().bmo_kv_ring_append_decode(
+            self._h, layer, n, _ptr(session_ids), _ptr(pos), n_heads, _ptr(q), _ptr(k), _ptr(v),
+            _ptr(out), float(scale), _stream(stream)))
+
+    def write(self, layer: int, session: int, pos0: int, k, v, n_tok=None, stream=None):
+        if n_tok is None:
+            n_tok = int(k.shape[0])
+        self._check("bmo_kv_ring_write", lib().bmo_kv_ring_write(
+            self._h, layer, session, int(pos0), int(n_tok), _ptr(k), _ptr(v), _stream(stream)))
+
+    @staticmethod
+    def _batch(pos, n_batch):
+        if n_batch is not None:
+            return int(n_batch)
+        if hasattr(pos, "numel"):
+            return int(pos.numel())
+        raise ValueError("n_batch is required when pos is a raw address")
+
+    # -- readout ------------------------------------------------------------------
+    def copy_k_cache_f32(self, layer: int, t_start: int, n_positions: int, out: np.ndarray,
+                         session: int = 0) -> int:
+        """The raw call (bmo_copy_k_cache_f32 contract): returns the count or a
+        negative code."""
+        assert out.dtype == np.float32 and out.flags["C_CONTIGUOUS"]
+        return int(lib().bmo_kv_ring_copy_k_f32(self._h, layer, session, t_start, n_positions,
+                                                out.ctypes.data, int(out.size)))
+
+    def get_k_cache_f32(self, layer: int, t_start: int, n_positions: int,
+                        session: int = 0) -> np.ndarray:
+        """K slots as float32, layout (n_positions, n_kv_heads, head_dim)
+        (bmo_engine.py:258-280)."""
+        n_el = int(n_positions) * self.n_kv_heads * self.head_dim
+        buf = np.empty(max(n_el, 1), dtype=np.float32)
+        n_written = self.copy_k_cache_f32(layer, t_start, n_positions, buf, session)
+        if n_written < 0:
+            raise RuntimeError(f"bmo_copy_k_cache_f32 failed with code {n_written}")
+        if n_written != n_el:
+            raise RuntimeError(f"bmo_copy_k_cache_f32 expected {n_el} floats, got {n_written}")
+        return buf[:n_el].reshape(int(n_positions), self.n_kv_heads, self.head_dim)
+
+    def export_q4_0(self, layer: int, session: int, which: int, t_start: int,
+                    n_positions: int) -> np.ndarray:
+        """ggml block_q4_0 bytes, shape (n_positions, n_kv_heads, head_dim/32, 18)."""
+        nblk = self.head_dim // 32
+        shape = (n_positions, self.n_kv_heads, nblk, BLOCK_Q4_0_BYTES)
+        buf = np.zeros(shape, dtype=np.uint8)
+        rc = lib().bmo_kv_ring_export_q4_0(self._h, layer, session, which, t_start, n_positions,
+                                           buf.ctypes.data, buf.size)
+        if rc < 0:
+            raise RuntimeError(f"bmo_kv_ring_export_q4_0 failed with code {rc}")
+        return buf
+
+    def import_q4_0(self, layer: int, session: int, which: int, t_start: int,
+                    blocks: np.ndarray) -> None:
+        blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+        nblk = self.head_dim // 32
+        n_positions = blocks.size // (self.n_kv_heads * nblk * BLOCK_Q4_0_BYTES)
+        rc = lib().bmo_kv_ring_import_q4_0(self._h, layer, session, which, t_start, n_positions,
+                                           blocks.ctypes.data, blocks.size)
+        if rc < 0:
+            raise RuntimeError(f"bmo_kv_ring_import_q4_0 failed with code {rc}")
+
+
+def launch_decode_attention(q, k, v, k_cache, v_cache, out, head_dim: int, n_heads: int,
+                            n_kv_heads: int, n_ctx: int, n_past: int, layer: int, stream=None,
+                            pos_dev=None) -> None:
+    """The node-level drop-in (reference launch_decode_attention signature)."""
+    lib().bmo_launch_decode_attention(_ptr(q), _ptr(k), _ptr(v), _ptr(k_cache), _ptr(v_cache),
+                                      _ptr(out), head_dim, n_heads, n_kv_heads, n_ctx, n_past,
+                                      layer, _stream(stream), _ptr(pos_dev))

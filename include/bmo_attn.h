@@ -1,0 +1,209 @@
+/*
+ * bmo_attn.h -- C ABI of the MI355X (gfx950) Q4_0 ring KV cache and its
+ * sliding-window attention kernels.
+ *
+ * Drop-in for the decode-attention path of utkarshyadav009/bmo_jetson:
+ *   - the KV allocator   bmo_init_kv_cache / bmo_reset_depth_kv
+ *                        (src/bmo.cpp:1348-1508, :1558-1565),
+ *   - the node launcher  launch_decode_attention (src/bmo.h:412-426,
+ *                        src/bmo_cuda_kernels.cu:713-884),
+ *   - the KV-touching parts of the public ABI bmo_reset and
+ *                        bmo_copy_k_cache_f32 (src/bmo_api.h:47,61-67).
+ *
+ * Conventions
+ *   - Plain C types only.  Device pointers are HIP device addresses, streams
+ *     are hipStream_t passed as void* (NULL = the null stream), exactly as the
+ *     reference passes cudaStream_t as void*.
+ *   - Every call is asynchronous on its stream unless it says otherwise.  Calls
+ *     on one ring must be ordered on one stream: the ring owns one split-merge
+ *     workspace, and two calls on one ring that overlap in time race on it.
+ *   - Functions returning int return BMO_ATTN_OK (0) or an error code below;
+ *     bmo_kv_ring_last_error() then describes the most recent failure on that
+ *     ring (as bmo_last_error does per handle, src/bmo_api.h:145).
+ *   - Q4_0 is ggml's block format (src/bmo_cuda_kernels.cu:496-499): 32
+ *     elements share one fp16 scale d, element j is (code_j - 8) * d, codes
+ *     are nibbles, element j in the low and j+16 in the high nibble of byte j.
+ *     Appends quantize bit-exactly as ggml quantize_row_q4_0_ref.
+ *
+ * Ring layout in HBM (what the kernels read; export/import convert to and
+ * from ggml's 18-byte AoS blocks):
+ *   two regions, K and V, each [n_layers][n_sessions][n_kv_heads] stripes of
+ *   bmo_kv_ring_stripe_bytes(head_dim, n_ctx) bytes; a stripe holds the
+ *   nibble plane [n_ctx][head_dim/2] bytes followed by the scale plane
+ *   [n_ctx][head_dim/32] fp16.  Slot of absolute position p is p % n_ctx.
+ */
+#ifndef BMO_ATTN_H
+#define BMO_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#if defined(__GNUC__) || defined(__clang__)
+#define BMO_ATTN_API __attribute__((visibility("default")))
+#else
+#define BMO_ATTN_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes.  1, 2 and 9 keep the meaning bmo_forward_temporal2 gives
+ * them (src/bmo_api.cpp:394-413, :504-510). */
+#define BMO_ATTN_OK 0
+#define BMO_ATTN_ERR_NULL 1      /* a required pointer argument is NULL */
+#define BMO_ATTN_ERR_ARG 2       /* an argument is out of range */
+#define BMO_ATTN_ERR_HIP 8       /* the HIP runtime reported an error */
+#define BMO_ATTN_ERR_INTERNAL 9  /* unexpected failure (exception) */
+
+/* Readout return codes of bmo_copy_k_cache_f32 (src/bmo_api.cpp:290-311). */
+#define BMO_ATTN_READ_ERR_NULL (-1)
+#define BMO_ATTN_READ_ERR_SMALL (-2)
+#define BMO_ATTN_READ_ERR_RANGE (-3)
+
+typedef struct bmo_kv_ring bmo_kv_ring_t;
+
+/* ---- allocation (replaces bmo_init_kv_cache, src/bmo.cpp:1348-1508) ------- */
+
+/* Bytes of one (layer, session, kv head) stripe of K (or of V). */
+BMO_ATTN_API int64_t bmo_kv_ring_stripe_bytes(int head_dim, int n_ctx);
+
+/* Allocates and zeroes a ring on the current HIP device.  head_dim must be 64
+ * or 128; n_ctx in [1, 65536] (no 1024 cap: that clamp, src/bmo.cpp:1362-1367,
+ * is an Orin memory budget).  The temporal cache of the reference is
+ * (32 layers, 1 session, 32 heads, 128, n_ctx); the depformer cache is
+ * (6, 1, 16, 64, 8).  Returns NULL on failure; bmo_kv_ring_last_error(NULL)
+ * then gives the reason (the calling thread's last create error). */
+BMO_ATTN_API bmo_kv_ring_t *bmo_kv_ring_create(int n_layers, int n_sessions,
+                                               int n_kv_heads, int head_dim,
+                                               int n_ctx);
+
+/* Releases the ring.  NULL-safe; never fails (src/bmo_api.cpp:210-256). */
+BMO_ATTN_API void bmo_kv_ring_free(bmo_kv_ring_t *ring);
+
+/* Geometry and allocation size; any output pointer may be NULL. */
+BMO_ATTN_API int bmo_kv_ring_geometry(const bmo_kv_ring_t *ring, int *n_layers,
+                                      int *n_sessions, int *n_kv_heads,
+                                      int *head_dim, int *n_ctx);
+BMO_ATTN_API int64_t bmo_kv_ring_bytes(const bmo_kv_ring_t *ring);
+
+/* Base addresses of the K and V regions, for bmo_launch_decode_attention. */
+BMO_ATTN_API void *bmo_kv_ring_k_base(bmo_kv_ring_t *ring);
+BMO_ATTN_API void *bmo_kv_ring_v_base(bmo_kv_ring_t *ring);
+
+/* Zeroes every layer of one session (session >= 0) or of all sessions
+ * (session == -1), asynchronously on stream.  A zeroed block dequantizes to
+ * 0.  Replaces the K/V memset of bmo_reset (src/bmo_api.cpp:258-272) and
+ * bmo_reset_depth_kv (src/bmo.cpp:1558-1565). */
+BMO_ATTN_API int bmo_kv_ring_reset(bmo_kv_ring_t *ring, int session,
+                                   void *stream);
+
+/* Message for the most recent failed call on ring, or for the calling
+ * thread's last failed bmo_kv_ring_create when ring is NULL.  NULL if none.
+ * Owned by the library, valid until the next call on the same ring/thread
+ * (src/bmo_api.h:142-145). */
+BMO_ATTN_API const char *bmo_kv_ring_last_error(const bmo_kv_ring_t *ring);
+
+/* ---- decode path ------------------------------------------------------------ */
+/*
+ * Batched forms: batch entry b (0 <= b < n_batch <= n_sessions) works on ring
+ * session session_ids[b] (or b when session_ids is NULL) at absolute position
+ * pos[b] >= 0.  session_ids and pos are DEVICE int arrays, so a captured graph
+ * can be replayed with new positions (the role of pos_dev in
+ * src/bmo_api.cpp:168-171).  An entry whose session id or position is out of
+ * range is skipped: nothing is written to the ring and its output rows are
+ * set to zero.
+ *   q, out:        [n_batch][n_heads][head_dim] fp32 (q after RoPE)
+ *   k_new, v_new:  [n_batch][n_kv_heads][head_dim] fp32
+ *   scale:         softmax scale; <= 0 selects 1/sqrt(head_dim)
+ *                  (src/bmo_cuda_kernels.cu:867)
+ * The window of position p is the min(p+1, n_ctx) most recent positions
+ * (src/bmo_cuda_kernels.cu:739-743).  n_heads must be a multiple of
+ * n_kv_heads; query head h reads kv head h / (n_heads / n_kv_heads)
+ * (src/bmo_cuda_kernels.cu:736-737).
+ */
+
+/* Quantizes k_new/v_new into slot pos[b] % n_ctx (the KV write of
+ * src/bmo_cuda_kernels.cu:749-754, to Q4_0 instead of fp16). */
+BMO_ATTN_API int bmo_kv_ring_append(bmo_kv_ring_t *ring, int layer, int n_batch,
+                                    const int *session_ids, const int *pos,
+                                    const float *k_new, const float *v_new,
+                                    void *stream);
+
+/* Attention of q over each entry's window as it stands in the ring (the
+ * current token must already have been appended). */
+BMO_ATTN_API int bmo_kv_ring_decode(bmo_kv_ring_t *ring, int layer, int n_batch,
+                                    const int *session_ids, const int *pos,
+                                    int n_heads, const float *q, float *out,
+                                    float scale, void *stream);
+
+/* Fused append + attention in one launch (the reference kernel's fused
+ * write-then-attend, src/bmo_cuda_kernels.cu:749-847): the current token's
+ * K/V are quantized, written to slot pos % n_ctx and attended to with their
+ * quantized values, together with the rest of the window. */
+BMO_ATTN_API int bmo_kv_ring_append_decode(bmo_kv_ring_t *ring, int layer,
+                                           int n_batch, const int *session_ids,
+                                           const int *pos, int n_heads,
+                                           const float *q, const float *k_new,
+                                           const float *v_new, float *out,
+                                           float scale, void *stream);
+
+/* Quantizes n_tok consecutive rows (positions pos0 .. pos0+n_tok-1, host
+ * values, 1 <= n_tok <= n_ctx) of one session into the ring.  k, v:
+ * [n_tok][n_kv_heads][head_dim] fp32 on the device.  This is the multi-token
+ * KV write of the reference's lazy path (src/bmo_compute.cpp:2390-2401), on
+ * ring slots. */
+BMO_ATTN_API int bmo_kv_ring_write(bmo_kv_ring_t *ring, int layer, int session,
+                                   int64_t pos0, int n_tok, const float *k,
+                                   const float *v, void *stream);
+
+/* ---- readout / export ------------------------------------------------------- */
+
+/* Copies slots [t_start, t_start+n_positions) of layer's K for one session as
+ * fp32 into HOST memory, layout (n_positions, n_kv_heads, head_dim); blocks
+ * until the copy is done (synchronizes the null stream's work on the ring's
+ * device first).  Returns the number of floats written, or -1 (NULL ring/out,
+ * n_positions <= 0, max_floats <= 0, bad session), -2 (max_floats too small),
+ * -3 (layer or slot range out of bounds), as bmo_copy_k_cache_f32 does
+ * (src/bmo_api.cpp:283-332; t_start is a slot index, not a position). */
+BMO_ATTN_API int bmo_kv_ring_copy_k_f32(bmo_kv_ring_t *ring, int layer,
+                                        int session, int t_start,
+                                        int n_positions, float *out,
+                                        int max_floats);
+
+/* Copies slots [t_start, t_start+n_positions) of K (which == 0) or V
+ * (which == 1) as ggml block_q4_0 (18 bytes per block, layout
+ * [n_positions][n_kv_heads][head_dim/32]) into HOST memory; synchronous.
+ * Returns bytes written or a negative readout code as above. */
+BMO_ATTN_API int64_t bmo_kv_ring_export_q4_0(bmo_kv_ring_t *ring, int layer,
+                                             int session, int which,
+                                             int t_start, int n_positions,
+                                             void *out, int64_t max_bytes);
+
+/* Inverse of export: writes host ggml blocks into the ring; synchronous. */
+BMO_ATTN_API int64_t bmo_kv_ring_import_q4_0(bmo_kv_ring_t *ring, int layer,
+                                             int session, int which,
+                                             int t_start, int n_positions,
+                                             const void *in, int64_t n_bytes);
+
+/* ---- node-level drop-in ------------------------------------------------------ */
+
+/* Same signature and semantics as the reference's launch_decode_attention
+ * (src/bmo.h:412-426, src/bmo_cuda_kernels.cu:850-884): fused write of the
+ * current k/v to slot (pos % n_ctx) and attention over the window, with
+ * pos = *pos_dev when pos_dev is non-NULL, else n_past.  k_cache_dev and
+ * v_cache_dev are bmo_kv_ring_k_base / bmo_kv_ring_v_base of a ring created
+ * with n_sessions == 1 and n_kv_heads == n_heads (the reference allocates
+ * n_heads head slots, src/bmo.cpp:1401-1402).  Returns nothing, as the
+ * reference does; launch errors surface through hipGetLastError(). */
+BMO_ATTN_API void bmo_launch_decode_attention(
+    const float *q_dev, const float *k_dev, const float *v_dev,
+    void *k_cache_dev, void *v_cache_dev, float *out_dev, int head_dim,
+    int n_heads, int n_kv_heads, int n_ctx, int n_past, int layer,
+    void *stream, const int *pos_dev);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BMO_ATTN_H */

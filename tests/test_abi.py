@@ -1,0 +1,79 @@
+"""CPU-side checks of the C ABI: the library loads, exports every function
+include/bmo_attn.h declares, and the error paths that need no GPU behave as
+the reference's ABI does (NULL-safe free, rc 1 for NULL, -1/-2/-3 readout
+codes, NULL + message from a rejected create).  No compute is launched."""
+import ctypes
+import subprocess
+
+import numpy as np
+import pytest
+
+import bmo_jetson_amd as bmo
+from bmo_jetson_amd import _lib
+
+
+def test_header_symbols_exported():
+    names = bmo.header_symbols()
+    assert len(names) >= 17
+    L = bmo.lib()
+    for n in names:
+        assert hasattr(L, n), n
+    out = subprocess.run(["nm", "-D", "--defined-only", bmo.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    assert set(names) <= exported
+    # nothing but the declared ABI is exported from the library's own code
+    ours = {s for s in exported if s.startswith("bmo")}
+    assert ours == set(names)
+    assert set(_lib.SIGNATURES) == set(names)
+
+
+def test_stripe_bytes():
+    L = bmo.lib()
+    # temporal: 512 slots * (64 code bytes + 8 scale bytes) = 36864 (a 256 multiple)
+    assert L.bmo_kv_ring_stripe_bytes(128, 512) == 512 * 72
+    # depformer: 8 * 36 = 288 -> padded to 512
+    assert L.bmo_kv_ring_stripe_bytes(64, 8) == 512
+    assert L.bmo_kv_ring_stripe_bytes(0, 8) == 0
+
+
+@pytest.mark.parametrize("args", [(0, 1, 1, 128, 8), (1, 0, 1, 128, 8), (1, 1, 0, 128, 8),
+                                  (1, 1, 1, 96, 8), (1, 1, 1, 128, 0), (1, 1, 1, 128, 65537)])
+def test_create_rejects_bad_geometry(args):
+    L = bmo.lib()
+    assert not L.bmo_kv_ring_create(*args)
+    err = L.bmo_kv_ring_last_error(None)
+    assert err and err.startswith(b"bmo_kv_ring_create:")
+
+
+def test_null_handle_paths():
+    L = bmo.lib()
+    L.bmo_kv_ring_free(None)  # NULL-safe, like bmo_free
+    assert L.bmo_kv_ring_geometry(None, None, None, None, None, None) == 1
+    assert L.bmo_kv_ring_bytes(None) == 0
+    assert L.bmo_kv_ring_k_base(None) is None
+    assert L.bmo_kv_ring_reset(None, -1, None) == 1
+    assert L.bmo_kv_ring_append(None, 0, 1, None, None, None, None, None) == 1
+    assert L.bmo_kv_ring_decode(None, 0, 1, None, None, 1, None, None, 0.0, None) == 1
+    assert L.bmo_kv_ring_append_decode(None, 0, 1, None, None, 1, None, None, None, None, 0.0,
+                                       None) == 1
+    assert L.bmo_kv_ring_write(None, 0, 0, 0, 1, None, None, None) == 1
+    buf = np.zeros(16, np.float32)
+    assert L.bmo_kv_ring_copy_k_f32(None, 0, 0, 0, 1, buf.ctypes.data, 16) == -1
+    assert L.bmo_kv_ring_export_q4_0(None, 0, 0, 0, 0, 1, buf.ctypes.data, 64) == -1
+    assert L.bmo_kv_ring_import_q4_0(None, 0, 0, 0, 0, 1, buf.ctypes.data, 64) == -1
+
+
+def test_node_launcher_rejects_bad_arguments_without_launching():
+    # every pointer NULL: returns without touching the device
+    bmo.launch_decode_attention(None, None, None, None, None, None, 128, 32, 32, 512, 0, 0)
+    # unsupported head_dim with non-NULL (never dereferenced) addresses
+    fake = 0x1000
+    bmo.launch_decode_attention(fake, fake, fake, fake, fake, fake, 96, 32, 32, 512, 0, 0)
+
+
+def test_package_fails_loudly_without_library(tmp_path, monkeypatch):
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "missing.so"))
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        _lib.lib()

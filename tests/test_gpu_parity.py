@@ -1,0 +1,319 @@
+"""GPU parity: the HIP kernels (called through the C ABI) against the CPU
+oracle on the same seeded inputs.
+
+  * append / write: bit-exact Q4_0 blocks (scale bits and code bytes);
+  * decode / fused append+decode / node launcher: within
+    |gpu - ref| <= 2e-3 + 1e-3 |ref| of the float64 oracle, and the ring
+    state after a fused call bit-exact.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from _ringsim import Mirror, check_close
+from bmo_jetson_amd import KVRing, launch_decode_attention, stripe_bytes
+
+pytestmark = pytest.mark.gpu
+
+KAT = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "q4_0_kat.json")))
+
+
+def _i32(torch, vals):
+    return torch.tensor(list(vals), dtype=torch.int32, device="cuda")
+
+
+def _adversarial_rows(n_rows, width, seed):
+    """Rows mixing the blocks most likely to expose a quantizer slip."""
+    rng = np.random.default_rng(seed)
+    nb = n_rows * width // 32
+    blocks = oracle.normal(seed, nb * 32).reshape(nb, 32)
+    kind = np.arange(nb) % 12
+    for i in range(nb):
+        x = blocks[i]
+        k = kind[i]
+        if k == 1:
+            x *= np.where(rng.random(32) < 0.05, 8.0, 1.0).astype(np.float32)
+        elif k == 2:
+            x[:] = 0.0
+        elif k == 3:
+            x[:] = -0.0
+        elif k == 4:
+            x[rng.integers(32)] = -np.abs(x).max() - 1.0
+            x[rng.integers(32)] = np.abs(x).max()  # magnitude tie, later index
+        elif k == 5:
+            x *= np.float32(2.0 ** rng.integers(-140, -120))  # subnormal / tiny scales
+        elif k == 6:
+            x *= np.float32(2.0 ** rng.integers(14, 20))       # fp16 overflowing scales
+        elif k == 7:
+            x[:] = np.round(x * 2) / 2                         # exact halves
+        elif k == 8:
+            x[:] = (np.arange(32) - 16).astype(np.float32) * np.float32(rng.random() + 0.1)
+        elif k == 9:
+            x[:] = np.float32(rng.random() + 0.5) * np.sign(x)  # constant magnitude
+        elif k == 10:
+            x *= np.float32(2.0 ** rng.integers(-30, -14))     # fp16-subnormal scales
+    return blocks.reshape(n_rows, width)
+
+
+@pytest.mark.parametrize("d", [128, 64])
+def test_write_bit_exact_kats(gpu, d):
+    cases = [np.array(c["x"], np.float32) for c in KAT["cases"]]
+    nblk = d // 32
+    n_kv = 2
+    rows = []
+    for r in range(0, len(cases), nblk * n_kv):
+        blocks = [cases[(r + i) % len(cases)] for i in range(nblk * n_kv)]
+        rows.append(np.concatenate(blocks).reshape(n_kv, d))
+    k = np.stack(rows)
+    v = -k[::-1].copy()
+    m = Mirror(gpu, 1, 1, n_kv, d, 16)
+    m.write(0, 0, 0, k, v)
+    gpu.cuda.synchronize()
+    m.assert_ring_equal(0, 0)
+
+
+@pytest.mark.parametrize("d,n_ctx", [(128, 512), (64, 8)])
+def test_write_bit_exact_adversarial(gpu, d, n_ctx):
+    n_kv = 4
+    m = Mirror(gpu, 2, 2, n_kv, d, n_ctx)
+    for layer in range(2):
+        for s in range(2):
+            n = n_ctx
+            k = _adversarial_rows(n * n_kv, d, 100 + layer * 10 + s).reshape(n, n_kv, d)
+            v = _adversarial_rows(n * n_kv, d, 200 + layer * 10 + s).reshape(n, n_kv, d)
+            m.write(layer, s, 1000 * s + layer, k, v)
+    gpu.cuda.synchronize()
+    for layer in range(2):
+        for s in range(2):
+            m.assert_ring_equal(layer, s)
+
+
+def test_append_batched_bit_exact(gpu):
+    n_sess, n_kv, d, n_ctx = 6, 8, 128, 32
+    m = Mirror(gpu, 1, n_sess, n_kv, d, n_ctx)
+    pos = [0, 31, 32, 77, 1000, 5]
+    sids = [3, 0, 5, 1, 4, 2]
+    k = _adversarial_rows(n_sess * n_kv, d, 7).reshape(n_sess, n_kv, d)
+    v = _adversarial_rows(n_sess * n_kv, d, 8).reshape(n_sess, n_kv, d)
+    m.ring.append(0, _i32(gpu, pos), m.dev(k), m.dev(v), session_ids=_i32(gpu, sids),
+                  stream=m.stream)
+    for b in range(n_sess):
+        m.oracle_append(0, sids[b], pos[b], k[b], v[b])
+    gpu.cuda.synchronize()
+    for s in range(n_sess):
+        m.assert_ring_equal(0, s)
+
+
+DECODE_CASES = [
+    # (n_heads, n_kv, d, n_ctx, pos)       config
+    (32, 32, 128, 512, 700),   # W=512, write head at 700 (slot 188)
+    (32, 32, 128, 512, 0),     # window of one key
+    (32, 32, 128, 512, 1),
+    (32, 32, 128, 512, 37),    # partial window
+    (32, 32, 128, 512, 510),
+    (32, 32, 128, 512, 511),   # ring exactly full
+    (32, 32, 128, 512, 512),   # first wrap
+    (32, 32, 128, 512, 4095),
+    (16, 16, 64, 8, 0),        # depformer, steps 1..8
+    (16, 16, 64, 8, 3),
+    (16, 16, 64, 8, 7),
+    (8, 2, 128, 64, 100),      # GQA
+    (4, 4, 128, 1000, 2500),   # n_ctx not a power of two
+    (4, 4, 64, 3, 10),         # tiny ring
+]
+
+
+@pytest.mark.parametrize("n_heads,n_kv,d,n_ctx,pos", DECODE_CASES)
+def test_decode_parity(gpu, n_heads, n_kv, d, n_ctx, pos):
+    m = Mirror(gpu, 2, 1, n_kv, d, n_ctx)
+    layer = 1
+    m.fill_range(layer, 0, 0, pos + 1, seed=0xB0A00001 + pos)  # whole window ending at pos
+    q = oracle.normal(0xB0A00001 ^ pos, n_heads * d)
+    out = gpu.empty(n_heads * d, dtype=gpu.float32, device="cuda")
+    m.ring.decode(layer, _i32(gpu, [pos]), m.dev(q), out, n_heads, stream=m.stream)
+    gpu.cuda.synchronize()
+    ref = m.oracle_decode(layer, 0, pos, q, n_heads)
+    check_close(out.cpu().numpy().reshape(n_heads, d), ref, f"decode pos={pos}")
+
+
+@pytest.mark.parametrize("n_heads,n_kv,d,n_ctx,pos", DECODE_CASES)
+def test_fused_append_decode_parity(gpu, n_heads, n_kv, d, n_ctx, pos):
+    m = Mirror(gpu, 2, 1, n_kv, d, n_ctx)
+    layer = 0
+    m.fill_range(layer, 0, 0, pos, seed=0xB0A00004 + pos)  # window before the new token
+    q = oracle.normal(11 + pos, n_heads * d)
+    k = oracle.normal(12 + pos, n_kv * d)
+    v = oracle.normal(13 + pos, n_kv * d)
+    out = gpu.empty(n_heads * d, dtype=gpu.float32, device="cuda")
+    m.ring.append_decode(layer, _i32(gpu, [pos]), m.dev(q), m.dev(k), m.dev(v), out, n_heads,
+                         stream=m.stream)
+    m.oracle_append(layer, 0, pos, k, v)
+    gpu.cuda.synchronize()
+    ref = m.oracle_decode(layer, 0, pos, q, n_heads)
+    check_close(out.cpu().numpy().reshape(n_heads, d), ref, f"fused pos={pos}")
+    m.assert_ring_equal(layer, 0)
+
+
+def test_batched_sessions_ids_and_invalid_entries(gpu):
+    n_sess, n_heads, d, n_ctx = 7, 8, 128, 96
+    m = Mirror(gpu, 1, n_sess, n_heads, d, n_ctx)
+    pos = [5, 95, 96, 300, 0, -1, 12]
+    sids = [6, 0, 2, 3, 1, 4, 9]  # entry 5 has pos -1, entry 6 a bad session id
+    for b, (s, p) in enumerate(zip(sids, pos)):
+        if 0 <= s < n_sess and p >= 0:
+            m.fill_range(0, s, 0, p, seed=300 + b)
+    before = {s: (m.ring.export_q4_0(0, s, 0, 0, n_ctx), m.ring.export_q4_0(0, s, 1, 0, n_ctx))
+              for s in (4, 5)}
+    q = oracle.normal(21, n_sess * n_heads * d).reshape(n_sess, n_heads, d)
+    k = oracle.normal(22, n_sess * n_heads * d).reshape(n_sess, n_heads, d)
+    v = oracle.normal(23, n_sess * n_heads * d).reshape(n_sess, n_heads, d)
+    out = gpu.full((n_sess, n_heads, d), 7.0, dtype=gpu.float32, device="cuda")
+    m.ring.append_decode(0, _i32(gpu, pos), m.dev(q), m.dev(k), m.dev(v), out, n_heads,
+                         session_ids=_i32(gpu, sids), stream=m.stream)
+    gpu.cuda.synchronize()
+    got = out.cpu().numpy()
+    for b, (s, p) in enumerate(zip(sids, pos)):
+        if 0 <= s < n_sess and p >= 0:
+            m.oracle_append(0, s, p, k[b], v[b])
+            check_close(got[b], m.oracle_decode(0, s, p, q[b], n_heads), f"entry {b}")
+            m.assert_ring_equal(0, s)
+        else:
+            assert np.all(got[b] == 0.0), f"skipped entry {b} must be zeroed"
+    for s in (4, 5):  # untouched sessions keep their bytes
+        assert np.array_equal(m.ring.export_q4_0(0, s, 0, 0, n_ctx), before[s][0])
+        assert np.array_equal(m.ring.export_q4_0(0, s, 1, 0, n_ctx), before[s][1])
+
+
+def test_sequence_of_steps_with_wrap(gpu):
+    """Autoregressive use: fused steps p = 0 .. 2*n_ctx+3 on one session, each
+    checked, so every slot is overwritten at least twice."""
+    n_heads, d, n_ctx = 4, 64, 16
+    m = Mirror(gpu, 1, 1, n_heads, d, n_ctx)
+    out = gpu.empty(n_heads * d, dtype=gpu.float32, device="cuda")
+    for p in range(2 * n_ctx + 4):
+        q = oracle.normal(1000 + p, n_heads * d)
+        k = oracle.normal(2000 + p, n_heads * d)
+        v = oracle.normal(3000 + p, n_heads * d)
+        m.ring.append_decode(0, _i32(gpu, [p]), m.dev(q), m.dev(k), m.dev(v), out, n_heads,
+                             stream=m.stream)
+        m.oracle_append(0, 0, p, k, v)
+        gpu.cuda.synchronize()
+        check_close(out.cpu().numpy().reshape(n_heads, d), m.oracle_decode(0, 0, p, q, n_heads),
+                    f"step {p}")
+    m.assert_ring_equal(0, 0)
+
+
+@pytest.mark.parametrize("use_pos_dev", [False, True])
+@pytest.mark.parametrize("n_heads,n_kv,d,n_ctx,pos", [(32, 32, 128, 512, 700), (16, 16, 64, 8, 5),
+                                                      (8, 4, 128, 32, 40)])
+def test_node_launcher(gpu, use_pos_dev, n_heads, n_kv, d, n_ctx, pos):
+    """bmo_launch_decode_attention over a ring allocated as the reference
+    allocates its cache (n_heads head slots, one session)."""
+    n_layers, layer = 3, 2
+    m = Mirror(gpu, n_layers, 1, n_heads, d, n_ctx)
+    # history for the n_kv live heads; the reference leaves slots >= n_kv unused
+    lo = max(0, pos - n_ctx + 1)
+    n = pos - lo
+    if n:
+        kh = np.zeros((n, n_heads, d), np.float32)
+        vh = np.zeros((n, n_heads, d), np.float32)
+        kh[:, :n_kv] = oracle.normal(41, n * n_kv * d).reshape(n, n_kv, d)
+        vh[:, :n_kv] = oracle.normal(42, n * n_kv * d).reshape(n, n_kv, d)
+        m.write(layer, 0, lo, kh, vh)
+    q = oracle.normal(43, n_heads * d)
+    k = oracle.normal(44, n_kv * d)
+    v = oracle.normal(45, n_kv * d)
+    out = gpu.empty(n_heads * d, dtype=gpu.float32, device="cuda")
+    pos_dev = _i32(gpu, [pos]) if use_pos_dev else None
+    launch_decode_attention(m.dev(q), m.dev(k), m.dev(v), m.ring.k_base, m.ring.v_base, out, d,
+                            n_heads, n_kv, n_ctx, 0 if use_pos_dev else pos, layer,
+                            stream=m.stream, pos_dev=pos_dev)
+    gpu.cuda.synchronize()
+    kc, vc = m.orc[(layer, 0)]
+    kfull = np.zeros((n_heads, d), np.float32)
+    vfull = np.zeros((n_heads, d), np.float32)
+    kfull[:n_kv] = k.reshape(n_kv, d)
+    vfull[:n_kv] = v.reshape(n_kv, d)
+    # the kernel writes kv heads 0..n_kv-1 only; mirror that
+    kq, vq = kc[:n_kv].copy(), vc[:n_kv].copy()
+    oracle.ring_append(kq, vq, pos, kfull[:n_kv], vfull[:n_kv])
+    ref = oracle.ring_decode_f64(kq, vq, pos, q, n_heads)
+    check_close(out.cpu().numpy().reshape(n_heads, d), ref, "node launcher")
+    kc[:n_kv], vc[:n_kv] = kq, vq
+    m.assert_ring_equal(layer, 0)
+
+
+def test_copy_k_cache_f32_and_codes(gpu):
+    n_kv, d, n_ctx = 4, 128, 40
+    m = Mirror(gpu, 2, 3, n_kv, d, n_ctx)
+    m.fill_range(1, 2, 0, 60, seed=51)
+    gpu.cuda.synchronize()
+    got = m.ring.get_k_cache_f32(1, 5, 30, session=2)
+    ref = oracle.ring_copy_k_f32(m.orc[(1, 2)][0], 5, 30)
+    assert np.array_equal(got, ref)
+    buf = np.zeros(10, np.float32)
+    assert m.ring.copy_k_cache_f32(1, 0, 1, buf, session=2) == -2         # too small
+    big = np.zeros(n_ctx * n_kv * d + 1, np.float32)
+    assert m.ring.copy_k_cache_f32(1, 30, 11, big, session=2) == -3       # slots past n_ctx
+    assert m.ring.copy_k_cache_f32(2, 0, 1, big, session=2) == -3         # bad layer
+    assert m.ring.copy_k_cache_f32(1, -1, 1, big, session=2) == -3
+    assert m.ring.copy_k_cache_f32(1, 0, 0, big, session=2) == -1         # n_positions <= 0
+    assert m.ring.copy_k_cache_f32(1, 0, 1, big, session=3) == -1         # bad session
+
+
+def test_reset_and_import_export(gpu):
+    n_kv, d, n_ctx = 2, 64, 8
+    m = Mirror(gpu, 2, 3, n_kv, d, n_ctx)
+    for s in range(3):
+        for layer in range(2):
+            m.fill_range(layer, s, 0, 9, seed=61 + s + 10 * layer)
+    gpu.cuda.synchronize()
+    snap = m.ring.export_q4_0(1, 1, 0, 0, n_ctx)
+    m.ring.reset(1, stream=m.stream)
+    gpu.cuda.synchronize()
+    for layer in range(2):
+        assert not m.ring.export_q4_0(layer, 1, 0, 0, n_ctx).any()
+        assert not m.ring.export_q4_0(layer, 1, 1, 0, n_ctx).any()
+        m.assert_ring_equal(layer, 0)
+        m.assert_ring_equal(layer, 2)
+    # a zeroed ring attends to zeros
+    out = gpu.empty(n_kv * d, dtype=gpu.float32, device="cuda")
+    m.ring.decode(0, _i32(gpu, [1, 5]), m.dev(oracle.normal(1, 2 * n_kv * d)), out, n_kv,
+                  n_batch=1, session_ids=_i32(gpu, [1]), stream=m.stream)
+    gpu.cuda.synchronize()
+    assert np.all(out.cpu().numpy() == 0.0)
+    m.ring.import_q4_0(1, 1, 0, 0, snap)
+    assert np.array_equal(m.ring.export_q4_0(1, 1, 0, 0, n_ctx), snap)
+    m.ring.reset(-1, stream=m.stream)
+    gpu.cuda.synchronize()
+    for s in range(3):
+        assert not m.ring.export_q4_0(0, s, 1, 0, n_ctx).any()
+
+
+def test_api_errors_on_device(gpu):
+    from bmo_jetson_amd import RingError
+    ring = KVRing(2, 2, 4, 128, 16)
+    pos = _i32(gpu, [0, 0])
+    x = gpu.zeros(2 * 4 * 128, dtype=gpu.float32, device="cuda")
+    with pytest.raises(RingError) as e:
+        ring.decode(2, pos, x, x, 4)
+    assert e.value.rc == 2 and "layer" in ring.last_error()
+    with pytest.raises(RingError) as e:
+        ring.decode(0, pos, x, x, 6)  # not a multiple of n_kv_heads
+    assert e.value.rc == 2
+    with pytest.raises(RingError) as e:
+        ring.append(0, pos, x, x, n_batch=3)
+    assert e.value.rc == 2
+    with pytest.raises(RingError) as e:
+        ring.write(0, 0, 0, x, x, n_tok=17)
+    assert e.value.rc == 2
+    with pytest.raises(RingError) as e:
+        ring.reset(5)
+    assert e.value.rc == 2
+    ring.decode(0, pos, x, x, 4)  # a good call clears the message
+    assert ring.last_error() is None
+    assert ring.geometry() == (2, 2, 4, 128, 16)
+    assert ring.nbytes == 2 * (2 * 2 * 4) * stripe_bytes(128, 16)
