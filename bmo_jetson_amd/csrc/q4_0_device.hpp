@@ -1,11 +1,15 @@
 // q4_0_device.hpp -- device-side Q4_0 block quantization, bit-exact with
 // ggml quantize_row_q4_0_ref as compiled for x86-64.
 //
-// Exactness rests on four properties of this build (checked in the ISA and by
-// the parity tests): fp32 division is correctly rounded (hipcc emits the
+// Exactness rests on properties of this build (checked in the ISA and by the
+// parity tests): fp32 division is correctly rounded (hipcc emits the
 // div_scale/div_fmas/div_fixup sequence), fp32 and fp16 denormals are kept
 // (float_denorm_mode 3), the fp32->fp16 conversion rounds to nearest even,
-// and no multiply-add below is contracted into an FMA.
+// and no multiply-add below is contracted into an FMA (the library is built
+// with -ffp-contract=off; kernels ask for FMAs explicitly with fmaf).  The
+// scale d is also pinned in a register before its fp16 conversion: otherwise
+// the backend folds fp16(m * -0.125) into a mixed-precision FMA with a +0
+// addend, which turns the -0.0 scale of an all-zero block into +0.0.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -52,7 +56,8 @@ __device__ __forceinline__ void quantize_block_q4_0(const float (&x)[kQK], uint1
             vmax = x[j];
         }
     }
-    const float d = vmax / -8.0f;
+    float d = vmax / -8.0f;
+    asm volatile("" : "+v"(d));  // materialize d in fp32 (see the header note)
     const float id = (d != 0.0f) ? 1.0f / d : 0.0f;
     d16 = f32_to_f16_bits(d);
 #pragma unroll
@@ -61,10 +66,10 @@ __device__ __forceinline__ void quantize_block_q4_0(const float (&x)[kQK], uint1
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int j = 4 * c + i;
-            const float p0 = __fmul_rn(x[j], id);
-            const float p1 = __fmul_rn(x[j + 16], id);
-            int c0 = x86_trunc_to_i8(__fadd_rn(p0, 8.5f));
-            int c1 = x86_trunc_to_i8(__fadd_rn(p1, 8.5f));
+            const float p0 = x[j] * id;
+            const float p1 = x[j + 16] * id;
+            int c0 = x86_trunc_to_i8(p0 + 8.5f);
+            int c1 = x86_trunc_to_i8(p1 + 8.5f);
             c0 = c0 > 15 ? 15 : c0;
             c1 = c1 > 15 ? 15 : c1;
             const uint32_t byte = ((uint32_t) c0 | ((uint32_t) c1 << 4)) & 0xFFu;
