@@ -24,11 +24,9 @@
 struct bmo_kv_ring {
     bmo::RingGeom g{};
     int device = 0;
-    uint8_t *mem = nullptr;  // K region, V region, split workspace, counters
+    uint8_t *mem = nullptr;  // K region then V region
     uint8_t *k_base = nullptr;
     uint8_t *v_base = nullptr;
-    float *partial = nullptr;
-    unsigned *counters = nullptr;
     std::mutex mu;  // guards last_error
     std::string last_error;
 };
@@ -74,23 +72,6 @@ int check_layer(bmo_kv_ring_t *r, int layer, const char *fn) {
     if (layer < 0 || layer >= r->g.n_layers)
         return fail(r, BMO_ATTN_ERR_ARG, std::string(fn) + ": layer out of range");
     return BMO_ATTN_OK;
-}
-
-// Window splits per (entry, head): enough workgroups to cover the GPU when
-// the batch is small, never fewer than 4 waves x one iteration of keys per
-// split.  BMO_ATTN_SPLIT overrides (tuning).
-int choose_split(const bmo::RingGeom &g, int units) {
-    static const int forced = [] {
-        const char *e = std::getenv("BMO_ATTN_SPLIT");
-        return e ? std::atoi(e) : 0;
-    }();
-    const int kpi = 64 / (g.head_dim / bmo::kQK);
-    const int min_keys = 4 * kpi;
-    int s = forced > 0 ? forced : std::max(1, 2048 / std::max(1, units));
-    s = std::min(s, std::max(1, g.n_ctx / min_keys));
-    s = std::min(s, bmo::kMaxSplit);
-    while (s > 1 && (int64_t) units * s > bmo::kMaxSplitUnits) --s;
-    return std::max(1, s);
 }
 
 float f16_to_f32_host(uint16_t h) {
@@ -165,9 +146,7 @@ bmo_kv_ring_t *bmo_kv_ring_create(int n_layers, int n_sessions, int n_kv_heads, 
             return reject("no HIP device");
         }
         const int64_t region = r->g.region_bytes();
-        const int64_t part_bytes = (int64_t) bmo::kMaxSplitUnits * (head_dim + 2) * 4;
-        const int64_t cnt_bytes = (int64_t) bmo::kMaxSplitUnits * 4;
-        const int64_t total = 2 * region + part_bytes + cnt_bytes;
+        const int64_t total = 2 * region;
         hipError_t e = hipMalloc(&r->mem, (size_t) total);
         if (e != hipSuccess) {
             delete r;
@@ -183,8 +162,6 @@ bmo_kv_ring_t *bmo_kv_ring_create(int n_layers, int n_sessions, int n_kv_heads, 
         }
         r->k_base = r->mem;
         r->v_base = r->mem + region;
-        r->partial = reinterpret_cast<float *>(r->mem + 2 * region);
-        r->counters = reinterpret_cast<unsigned *>(r->mem + 2 * region + part_bytes);
         return r;
     } catch (const std::exception &ex) {
         return reject(ex.what());
@@ -319,7 +296,6 @@ static int decode_common(bmo_kv_ring_t *r, const char *fn, bool fused, int layer
         p.n_batch = n_batch;
         p.n_heads = n_heads;
         p.n_kv = r->g.n_kv_heads;
-        p.n_split = choose_split(r->g, n_batch * n_heads);
         p.session_ids = session_ids;
         p.pos = pos;
         p.q = q;
@@ -327,8 +303,6 @@ static int decode_common(bmo_kv_ring_t *r, const char *fn, bool fused, int layer
         p.v_new = v_new;
         p.out = out;
         p.qscale = scale * kLog2e;
-        p.partial = r->partial;
-        p.counters = r->counters;
         if (!bmo::launch_decode(p, fused, (hipStream_t) stream))
             return fail(r, BMO_ATTN_ERR_ARG, std::string(fn) + ": unsupported head_dim");
         hipError_t e = hipGetLastError();
@@ -526,7 +500,6 @@ void bmo_launch_decode_attention(const float *q_dev, const float *k_dev, const f
     p.n_batch = 1;
     p.n_heads = n_heads;
     p.n_kv = n_kv_heads;
-    p.n_split = 1;
     p.pos = pos_dev;
     p.pos_scalar = n_past;
     p.q = q_dev;

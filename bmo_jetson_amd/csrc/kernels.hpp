@@ -39,7 +39,6 @@ struct DecodeParams {
     int n_heads;
     int n_kv;                // logical kv heads: GQA map and k_new/v_new row stride
                              // (g.n_kv_heads is the allocated head count per stripe set)
-    int n_split;             // workgroups per (entry, head); 1 = no merge pass
     const int *session_ids;  // device, nullable
     const int *pos;          // device [n_batch], or nullptr -> pos_scalar
     int pos_scalar;
@@ -48,17 +47,11 @@ struct DecodeParams {
     const float *v_new;
     float *out;          // [n_batch][n_heads][head_dim]
     float qscale;        // softmax scale * log2(e)
-    float *partial;      // [n_batch*n_heads][n_split][head_dim + 2] (n_split > 1)
-    unsigned *counters;  // [n_batch*n_heads], zero between launches (n_split > 1)
 };
 
 // Launchers enqueue only; they leave launch errors for the caller's
 // hipGetLastError().  launch_decode returns false for an unsupported head_dim.
 void launch_append(const AppendParams &p, hipStream_t stream);
 bool launch_decode(const DecodeParams &p, bool fused, hipStream_t stream);
-
-// Largest (entry, head) unit count times n_split the split workspace covers.
-constexpr int kMaxSplitUnits = 16384;
-constexpr int kMaxSplit = 16;
 
 }  // namespace bmo

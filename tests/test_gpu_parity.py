@@ -132,7 +132,7 @@ def test_decode_parity(gpu, n_heads, n_kv, d, n_ctx, pos):
     layer = 1
     m.fill_range(layer, 0, 0, pos + 1, seed=0xB0A00001 + pos)  # whole window ending at pos
     q = oracle.normal(0xB0A00001 ^ pos, n_heads * d)
-    out = gpu.empty(n_heads * d, dtype=gpu.float32, device="cuda")
+    out = gpu.full((n_heads * d,), float("nan"), dtype=gpu.float32, device="cuda")
     m.ring.decode(layer, _i32(gpu, [pos]), m.dev(q), out, n_heads, stream=m.stream)
     gpu.cuda.synchronize()
     ref = m.oracle_decode(layer, 0, pos, q, n_heads)
@@ -147,7 +147,7 @@ def test_fused_append_decode_parity(gpu, n_heads, n_kv, d, n_ctx, pos):
     q = oracle.normal(11 + pos, n_heads * d)
     k = oracle.normal(12 + pos, n_kv * d)
     v = oracle.normal(13 + pos, n_kv * d)
-    out = gpu.empty(n_heads * d, dtype=gpu.float32, device="cuda")
+    out = gpu.full((n_heads * d,), float("nan"), dtype=gpu.float32, device="cuda")
     m.ring.append_decode(layer, _i32(gpu, [pos]), m.dev(q), m.dev(k), m.dev(v), out, n_heads,
                          stream=m.stream)
     m.oracle_append(layer, 0, pos, k, v)
@@ -192,7 +192,7 @@ def test_sequence_of_steps_with_wrap(gpu):
     checked, so every slot is overwritten at least twice."""
     n_heads, d, n_ctx = 4, 64, 16
     m = Mirror(gpu, 1, 1, n_heads, d, n_ctx)
-    out = gpu.empty(n_heads * d, dtype=gpu.float32, device="cuda")
+    out = gpu.full((n_heads * d,), float("nan"), dtype=gpu.float32, device="cuda")
     for p in range(2 * n_ctx + 4):
         q = oracle.normal(1000 + p, n_heads * d)
         k = oracle.normal(2000 + p, n_heads * d)
@@ -226,7 +226,7 @@ def test_node_launcher(gpu, use_pos_dev, n_heads, n_kv, d, n_ctx, pos):
     q = oracle.normal(43, n_heads * d)
     k = oracle.normal(44, n_kv * d)
     v = oracle.normal(45, n_kv * d)
-    out = gpu.empty(n_heads * d, dtype=gpu.float32, device="cuda")
+    out = gpu.full((n_heads * d,), float("nan"), dtype=gpu.float32, device="cuda")
     pos_dev = _i32(gpu, [pos]) if use_pos_dev else None
     launch_decode_attention(m.dev(q), m.dev(k), m.dev(v), m.ring.k_base, m.ring.v_base, out, d,
                             n_heads, n_kv, n_ctx, 0 if use_pos_dev else pos, layer,
@@ -317,3 +317,74 @@ def test_api_errors_on_device(gpu):
     assert ring.last_error() is None
     assert ring.geometry() == (2, 2, 4, 128, 16)
     assert ring.nbytes == 2 * (2 * 2 * 4) * stripe_bytes(128, 16)
+
+
+# every shape compiled into launch_shape() (decode.hip)
+SHAPES = ["4,4,0,0", "4,2,1,0", "4,4,1,0", "1,4,1,1", "1,4,2,1", "1,2,2,1", "1,2,3,1", "1,8,1,1",
+          "2,4,1,1", "2,2,2,1"]
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("d,n_ctx,pos", [(128, 512, 700), (128, 512, 130), (64, 8, 5), (64, 200, 450)])
+@pytest.mark.parametrize("fused", [False, True])
+def test_every_workgroup_shape(gpu, monkeypatch, shape, d, n_ctx, pos, fused):
+    """Each compiled workgroup shape (waves, tile, prefetch depth, K scorer),
+    forced through BMO_ATTN_SHAPE, against the oracle."""
+    monkeypatch.setenv("BMO_ATTN_SHAPE", shape)
+    n_sess, n_heads, n_kv = 3, 8, 4
+    m = Mirror(gpu, 1, n_sess, n_kv, d, n_ctx)
+    # output buffers start as NaN so an element the kernel never writes fails
+    poss = [pos, max(0, pos - 3), pos + 17]
+    for s, p in enumerate(poss):
+        m.fill_range(0, s, 0, p + (0 if fused else 1), seed=500 + s)
+    q = oracle.normal(31, n_sess * n_heads * d).reshape(n_sess, n_heads, d)
+    out = gpu.full((n_sess, n_heads, d), float("nan"), dtype=gpu.float32, device="cuda")
+    if fused:
+        k = oracle.normal(32, n_sess * n_kv * d).reshape(n_sess, n_kv, d)
+        v = oracle.normal(33, n_sess * n_kv * d).reshape(n_sess, n_kv, d)
+        m.ring.append_decode(0, _i32(gpu, poss), m.dev(q), m.dev(k), m.dev(v), out, n_heads,
+                             stream=m.stream)
+        for s, p in enumerate(poss):
+            m.oracle_append(0, s, p, k[s], v[s])
+    else:
+        m.ring.decode(0, _i32(gpu, poss), m.dev(q), out, n_heads, stream=m.stream)
+    gpu.cuda.synchronize()
+    got = out.cpu().numpy()
+    for s, p in enumerate(poss):
+        check_close(got[s], m.oracle_decode(0, s, p, q[s], n_heads), f"shape {shape} entry {s}")
+    if fused:
+        for s in range(n_sess):
+            m.assert_ring_equal(0, s)
+
+
+@pytest.mark.parametrize("fused", [False, True])
+def test_large_batch_default_shape(gpu, fused):
+    """>= 512 (entry, head) units selects the batch shape (one wave per unit,
+    fixed-point K scorer): 64 sessions x 8 heads, random wrap points."""
+    n_sess, n_heads, d, n_ctx = 64, 8, 128, 128
+    m = Mirror(gpu, 2, n_sess, n_heads, d, n_ctx)
+    rng = np.random.default_rng(5)
+    poss = [int(x) for x in rng.integers(0, 3 * n_ctx, size=n_sess)]
+    layer = 1
+    for s, p in enumerate(poss):
+        m.fill_range(layer, s, 0, p + (0 if fused else 1), seed=700 + s)
+    q = oracle.normal(41, n_sess * n_heads * d).reshape(n_sess, n_heads, d)
+    out = gpu.full((n_sess, n_heads, d), float("nan"), dtype=gpu.float32, device="cuda")
+    if fused:
+        k = oracle.normal(42, n_sess * n_heads * d).reshape(n_sess, n_heads, d)
+        v = oracle.normal(43, n_sess * n_heads * d).reshape(n_sess, n_heads, d)
+        m.ring.append_decode(layer, _i32(gpu, poss), m.dev(q), m.dev(k), m.dev(v), out, n_heads,
+                             stream=m.stream)
+        for s, p in enumerate(poss):
+            m.oracle_append(layer, s, p, k[s], v[s])
+    else:
+        m.ring.decode(layer, _i32(gpu, poss), m.dev(q), out, n_heads, stream=m.stream)
+    gpu.cuda.synchronize()
+    got = out.cpu().numpy()
+    worst = 0.0
+    for s, p in enumerate(poss):
+        mx, _ = check_close(got[s], m.oracle_decode(layer, s, p, q[s], n_heads), f"session {s}")
+        worst = max(worst, mx)
+    if fused:
+        for s in range(0, n_sess, 7):
+            m.assert_ring_equal(layer, s)
