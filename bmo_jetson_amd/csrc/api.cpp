@@ -14,6 +14,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <exception>
+#include <map>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -24,16 +25,25 @@
 struct bmo_kv_ring {
     bmo::RingGeom g{};
     int device = 0;
-    uint8_t *mem = nullptr;  // K region then V region
-    uint8_t *k_base = nullptr;
-    uint8_t *v_base = nullptr;
-    std::mutex mu;  // guards last_error
+    uint8_t *mem = nullptr;  // every stripe (layout in ring_layout.hpp)
+    std::mutex mu;           // guards last_error
     std::string last_error;
 };
 
 namespace {
 
 thread_local std::string t_create_error;
+
+// Rings by base address, so the node-level launcher (which only receives the
+// cache pointers, as the reference's does) can check a ring's geometry.
+std::mutex g_registry_mu;
+std::map<const void *, bmo_kv_ring_t *> g_registry;
+
+bmo_kv_ring_t *registry_find(const void *base) {
+    std::lock_guard<std::mutex> lk(g_registry_mu);
+    auto it = g_registry.find(base);
+    return it == g_registry.end() ? nullptr : it->second;
+}
 
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -93,28 +103,38 @@ float f16_to_f32_host(uint16_t h) {
     return f;
 }
 
-// Copies the nibble and scale rows of slots [t0, t0+n) of one stripe to host.
-hipError_t fetch_rows(const bmo_kv_ring_t *r, const uint8_t *stripe, int t0, int n,
-                      std::vector<uint8_t> &nib, std::vector<uint16_t> &scl) {
-    const int D = r->g.head_dim;
-    nib.resize((size_t) n * D / 2);
-    scl.resize((size_t) n * (D / bmo::kQK));
-    hipError_t e = hipMemcpy(nib.data(), stripe + (int64_t) t0 * D / 2, nib.size(), hipMemcpyDeviceToHost);
-    if (e != hipSuccess) return e;
-    return hipMemcpy(scl.data(), stripe + r->g.nib_bytes + (int64_t) t0 * (D / bmo::kQK) * 2,
-                     scl.size() * 2, hipMemcpyDeviceToHost);
+// Copies the groups holding slots [t0, t0+n) of one stripe to host; *first
+// receives the first group's index.
+hipError_t fetch_groups(const bmo_kv_ring_t *r, const uint8_t *stripe, int t0, int n,
+                        std::vector<uint8_t> &buf, int *first) {
+    const int G = bmo::keys_per_group(r->g.head_dim);
+    const int g0 = t0 / G, g1 = (t0 + n - 1) / G;
+    *first = g0;
+    buf.resize((size_t) (g1 - g0 + 1) * bmo::kGroupBytes);
+    return hipMemcpy(buf.data(), stripe + (int64_t) g0 * bmo::kGroupBytes, buf.size(),
+                     hipMemcpyDeviceToHost);
 }
 
-__global__ void zero_ranges_kernel(uint8_t *base, int64_t range_bytes, int64_t range_stride,
-                                   int64_t v_offset) {
-    // blockIdx.y selects (region, range); ranges are 16-byte multiples.
-    const int64_t range = blockIdx.y >> 1;
-    uint8_t *start = base + range * range_stride + ((blockIdx.y & 1) ? v_offset : 0);
-    uint4 *p = reinterpret_cast<uint4 *>(start);
-    const int64_t n = range_bytes / 16;
-    for (int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; i < n;
-         i += (int64_t) gridDim.x * blockDim.x)
-        p[i] = make_uint4(0, 0, 0, 0);
+// ggml block (scale bits, 16 code bytes) of K (which 0) or V (which 1) at
+// slot, block blk, from a host copy of groups starting at group `first`.
+void read_block(const bmo::RingGeom &g, const std::vector<uint8_t> &buf, int first, int which,
+                int slot, int blk, uint16_t *d, uint8_t *qs) {
+    const int64_t base = (int64_t) first * bmo::kGroupBytes;
+    const uint8_t *codes = buf.data() + (which == 0 ? g.kcode_offset(slot, blk)
+                                                     : g.vcode_offset(slot, blk)) - base;
+    const uint8_t flip = which == 0 ? bmo::kKCodeZero : 0;
+    for (int j = 0; j < 16; ++j) qs[j] = codes[j] ^ flip;
+    std::memcpy(d, buf.data() + g.scale_offset(slot, blk) - base + 2 * which, 2);
+}
+
+void write_block(const bmo::RingGeom &g, std::vector<uint8_t> &buf, int first, int which,
+                 int slot, int blk, uint16_t d, const uint8_t *qs) {
+    const int64_t base = (int64_t) first * bmo::kGroupBytes;
+    uint8_t *codes = buf.data() + (which == 0 ? g.kcode_offset(slot, blk)
+                                               : g.vcode_offset(slot, blk)) - base;
+    const uint8_t flip = which == 0 ? bmo::kKCodeZero : 0;
+    for (int j = 0; j < 16; ++j) codes[j] = qs[j] ^ flip;
+    std::memcpy(buf.data() + g.scale_offset(slot, blk) - base + 2 * which, &d, 2);
 }
 
 }  // namespace
@@ -122,7 +142,7 @@ __global__ void zero_ranges_kernel(uint8_t *base, int64_t range_bytes, int64_t r
 extern "C" {
 
 int64_t bmo_kv_ring_stripe_bytes(int head_dim, int n_ctx) {
-    if (head_dim <= 0 || n_ctx <= 0) return 0;
+    if ((head_dim != 64 && head_dim != 128) || n_ctx <= 0) return 0;
     return bmo::stripe_bytes_for(head_dim, n_ctx);
 }
 
@@ -138,34 +158,42 @@ bmo_kv_ring_t *bmo_kv_ring_create(int n_layers, int n_sessions, int n_kv_heads, 
         return reject("n_layers, n_sessions and n_kv_heads must be positive");
     if (head_dim != 64 && head_dim != 128) return reject("head_dim must be 64 or 128");
     if (n_ctx <= 0 || n_ctx > 65536) return reject("n_ctx must be in [1, 65536]");
+    bmo_kv_ring_t *r = nullptr;
+    auto release = [](bmo_kv_ring_t *x) {
+        if (x->mem) (void) hipFree(x->mem);
+        delete x;
+    };
     try {
-        auto *r = new bmo_kv_ring();
+        r = new bmo_kv_ring();
         r->g = bmo::make_geom(n_layers, n_sessions, n_kv_heads, head_dim, n_ctx);
         if (hipGetDevice(&r->device) != hipSuccess) {
             delete r;
             return reject("no HIP device");
         }
-        const int64_t region = r->g.region_bytes();
-        const int64_t total = 2 * region;
+        const int64_t total = r->g.total_bytes();
         hipError_t e = hipMalloc(&r->mem, (size_t) total);
         if (e != hipSuccess) {
-            delete r;
+            r->mem = nullptr;
+            release(r);
             return reject(std::string("hipMalloc of ") + std::to_string(total) +
                           " bytes failed: " + hipGetErrorString(e));
         }
-        e = hipMemset(r->mem, 0, (size_t) total);
+        bmo::launch_clear(r->mem, total, 0, 1, nullptr);
+        e = hipGetLastError();
         if (e == hipSuccess) e = hipDeviceSynchronize();
         if (e != hipSuccess) {
-            (void) hipFree(r->mem);
-            delete r;
-            return reject(std::string("hipMemset failed: ") + hipGetErrorString(e));
+            release(r);
+            return reject(std::string("allocation or initialisation failed: ") +
+                          hipGetErrorString(e));
         }
-        r->k_base = r->mem;
-        r->v_base = r->mem + region;
+        std::lock_guard<std::mutex> lk(g_registry_mu);
+        g_registry[r->mem] = r;
         return r;
     } catch (const std::exception &ex) {
+        if (r) release(r);
         return reject(ex.what());
     } catch (...) {
+        if (r) release(r);
         return reject("unknown exception");
     }
 }
@@ -173,6 +201,10 @@ bmo_kv_ring_t *bmo_kv_ring_create(int n_layers, int n_sessions, int n_kv_heads, 
 void bmo_kv_ring_free(bmo_kv_ring_t *ring) {
     if (!ring) return;
     try {
+        {
+            std::lock_guard<std::mutex> lk(g_registry_mu);
+            g_registry.erase(ring->mem);
+        }
         DeviceGuard dg(ring->device);
         if (ring->mem) (void) hipFree(ring->mem);
     } catch (...) {
@@ -191,10 +223,10 @@ int bmo_kv_ring_geometry(const bmo_kv_ring_t *r, int *n_layers, int *n_sessions,
     return BMO_ATTN_OK;
 }
 
-int64_t bmo_kv_ring_bytes(const bmo_kv_ring_t *r) { return r ? 2 * r->g.region_bytes() : 0; }
+int64_t bmo_kv_ring_bytes(const bmo_kv_ring_t *r) { return r ? r->g.total_bytes() : 0; }
 
-void *bmo_kv_ring_k_base(bmo_kv_ring_t *r) { return r ? r->k_base : nullptr; }
-void *bmo_kv_ring_v_base(bmo_kv_ring_t *r) { return r ? r->v_base : nullptr; }
+void *bmo_kv_ring_k_base(bmo_kv_ring_t *r) { return r ? r->mem : nullptr; }
+void *bmo_kv_ring_v_base(bmo_kv_ring_t *r) { return r ? r->mem + bmo::kVCodeOff : nullptr; }
 
 const char *bmo_kv_ring_last_error(const bmo_kv_ring_t *r) {
     if (!r) return t_create_error.empty() ? nullptr : t_create_error.c_str();
@@ -210,25 +242,15 @@ int bmo_kv_ring_reset(bmo_kv_ring_t *r, int session, void *stream) {
             return fail(r, BMO_ATTN_ERR_ARG, "bmo_kv_ring_reset: session out of range");
         DeviceGuard dg(r->device);
         const bmo::RingGeom &g = r->g;
-        int64_t range_bytes, stride;
-        unsigned n_ranges;
-        uint8_t *base;
         if (session == -1) {
-            base = r->k_base;
-            range_bytes = g.region_bytes();
-            stride = 0;
-            n_ranges = 1;
+            bmo::launch_clear(r->mem, g.total_bytes(), 0, 1, (hipStream_t) stream);
         } else {
             // session s of layer l: n_kv_heads contiguous stripes
-            base = r->k_base + g.stripe_offset(0, session, 0);
-            range_bytes = (int64_t) g.n_kv_heads * g.stripe_bytes;
-            stride = (int64_t) g.n_sessions * g.n_kv_heads * g.stripe_bytes;
-            n_ranges = (unsigned) g.n_layers;
+            bmo::launch_clear(r->mem + g.stripe_offset(0, session, 0),
+                              (int64_t) g.n_kv_heads * g.stripe_bytes,
+                              (int64_t) g.n_sessions * g.n_kv_heads * g.stripe_bytes, g.n_layers,
+                              (hipStream_t) stream);
         }
-        const int64_t vecs = range_bytes / 16;
-        const unsigned gx = (unsigned) std::min<int64_t>((vecs + 255) / 256, 4096);
-        hipLaunchKernelGGL(zero_ranges_kernel, dim3(gx, 2 * n_ranges), dim3(256), 0,
-                           (hipStream_t) stream, base, range_bytes, stride, g.region_bytes());
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return hip_fail(r, e, "bmo_kv_ring_reset");
         clear_error(r);
@@ -249,8 +271,7 @@ int bmo_kv_ring_append(bmo_kv_ring_t *r, int layer, int n_batch, const int *sess
             return fail(r, BMO_ATTN_ERR_ARG, "bmo_kv_ring_append: n_batch must be in [1, n_sessions]");
         DeviceGuard dg(r->device);
         bmo::AppendParams p{};
-        p.k_base = r->k_base;
-        p.v_base = r->v_base;
+        p.base = r->mem;
         p.g = r->g;
         p.layer = layer;
         p.n_rows = n_batch;
@@ -287,10 +308,7 @@ static int decode_common(bmo_kv_ring_t *r, const char *fn, bool fused, int layer
             return fail(r, BMO_ATTN_ERR_ARG, std::string(fn) + ": scale must be finite");
         DeviceGuard dg(r->device);
         bmo::DecodeParams p{};
-        p.k_base = r->k_base;
-        p.v_base = r->v_base;
-        p.k_wbase = r->k_base;
-        p.v_wbase = r->v_base;
+        p.base = r->mem;
         p.g = r->g;
         p.layer = layer;
         p.n_batch = n_batch;
@@ -341,8 +359,7 @@ int bmo_kv_ring_write(bmo_kv_ring_t *r, int layer, int session, int64_t pos0, in
             return fail(r, BMO_ATTN_ERR_ARG, "bmo_kv_ring_write: n_tok must be in [1, n_ctx]");
         DeviceGuard dg(r->device);
         bmo::AppendParams p{};
-        p.k_base = r->k_base;
-        p.v_base = r->v_base;
+        p.base = r->mem;
         p.g = r->g;
         p.layer = layer;
         p.n_rows = n_tok;
@@ -374,17 +391,19 @@ int bmo_kv_ring_copy_k_f32(bmo_kv_ring_t *r, int layer, int session, int t_start
         if (hipDeviceSynchronize() != hipSuccess) return BMO_ATTN_READ_ERR_NULL;
         const int D = g.head_dim;
         const int nblk = D / bmo::kQK;
-        std::vector<uint8_t> nib;
-        std::vector<uint16_t> scl;
+        std::vector<uint8_t> buf;
+        int first = 0;
         for (int h = 0; h < g.n_kv_heads; ++h) {
-            const uint8_t *stripe = r->k_base + g.stripe_offset(layer, session, h);
-            if (fetch_rows(r, stripe, t_start, n_positions, nib, scl) != hipSuccess)
+            if (fetch_groups(r, r->mem + g.stripe_offset(layer, session, h), t_start, n_positions,
+                             buf, &first) != hipSuccess)
                 return BMO_ATTN_READ_ERR_NULL;
             for (int ti = 0; ti < n_positions; ++ti) {
                 float *o = out + ((int64_t) ti * g.n_kv_heads + h) * D;
                 for (int b = 0; b < nblk; ++b) {
-                    const float d = f16_to_f32_host(scl[(size_t) ti * nblk + b]);
-                    const uint8_t *qs = nib.data() + (size_t) ti * D / 2 + b * 16;
+                    uint16_t d16;
+                    uint8_t qs[16];
+                    read_block(g, buf, first, 0, t_start + ti, b, &d16, qs);
+                    const float d = f16_to_f32_host(d16);
                     for (int j = 0; j < 16; ++j) {
                         o[b * 32 + j] = (float) ((int) (qs[j] & 0x0F) - 8) * d;
                         o[b * 32 + j + 16] = (float) ((int) (qs[j] >> 4) - 8) * d;
@@ -413,18 +432,18 @@ int64_t bmo_kv_ring_export_q4_0(bmo_kv_ring_t *r, int layer, int session, int wh
         DeviceGuard dg(r->device);
         if (hipDeviceSynchronize() != hipSuccess) return BMO_ATTN_READ_ERR_NULL;
         uint8_t *dst = static_cast<uint8_t *>(out);
-        std::vector<uint8_t> nib;
-        std::vector<uint16_t> scl;
-        const uint8_t *base = which == 0 ? r->k_base : r->v_base;
+        std::vector<uint8_t> buf;
+        int first = 0;
         for (int h = 0; h < g.n_kv_heads; ++h) {
-            if (fetch_rows(r, base + g.stripe_offset(layer, session, h), t_start, n_positions, nib,
-                           scl) != hipSuccess)
+            if (fetch_groups(r, r->mem + g.stripe_offset(layer, session, h), t_start, n_positions,
+                             buf, &first) != hipSuccess)
                 return BMO_ATTN_READ_ERR_NULL;
             for (int ti = 0; ti < n_positions; ++ti)
                 for (int b = 0; b < nblk; ++b) {
                     uint8_t *blkp = dst + (((int64_t) ti * g.n_kv_heads + h) * nblk + b) * 18;
-                    std::memcpy(blkp, &scl[(size_t) ti * nblk + b], 2);
-                    std::memcpy(blkp + 2, nib.data() + (size_t) ti * g.head_dim / 2 + b * 16, 16);
+                    uint16_t d16;
+                    read_block(g, buf, first, which, t_start + ti, b, &d16, blkp + 2);
+                    std::memcpy(blkp, &d16, 2);
                 }
         }
         return need;
@@ -448,21 +467,23 @@ int64_t bmo_kv_ring_import_q4_0(bmo_kv_ring_t *r, int layer, int session, int wh
         DeviceGuard dg(r->device);
         if (hipDeviceSynchronize() != hipSuccess) return BMO_ATTN_READ_ERR_NULL;
         const uint8_t *src = static_cast<const uint8_t *>(in);
-        std::vector<uint8_t> nib((size_t) n_positions * g.head_dim / 2);
-        std::vector<uint16_t> scl((size_t) n_positions * nblk);
-        uint8_t *base = which == 0 ? r->k_base : r->v_base;
+        std::vector<uint8_t> buf;
+        int first = 0;
         for (int h = 0; h < g.n_kv_heads; ++h) {
+            uint8_t *stripe = r->mem + g.stripe_offset(layer, session, h);
+            // read-modify-write: a group also holds other slots and the other
+            // half of each scale dword
+            if (fetch_groups(r, stripe, t_start, n_positions, buf, &first) != hipSuccess)
+                return BMO_ATTN_READ_ERR_NULL;
             for (int ti = 0; ti < n_positions; ++ti)
                 for (int b = 0; b < nblk; ++b) {
                     const uint8_t *blkp = src + (((int64_t) ti * g.n_kv_heads + h) * nblk + b) * 18;
-                    std::memcpy(&scl[(size_t) ti * nblk + b], blkp, 2);
-                    std::memcpy(nib.data() + (size_t) ti * g.head_dim / 2 + b * 16, blkp + 2, 16);
+                    uint16_t d16;
+                    std::memcpy(&d16, blkp, 2);
+                    write_block(g, buf, first, which, t_start + ti, b, d16, blkp + 2);
                 }
-            uint8_t *stripe = base + g.stripe_offset(layer, session, h);
-            if (hipMemcpy(stripe + (int64_t) t_start * g.head_dim / 2, nib.data(), nib.size(),
-                          hipMemcpyHostToDevice) != hipSuccess ||
-                hipMemcpy(stripe + g.nib_bytes + (int64_t) t_start * nblk * 2, scl.data(),
-                          scl.size() * 2, hipMemcpyHostToDevice) != hipSuccess)
+            if (hipMemcpy(stripe + (int64_t) first * bmo::kGroupBytes, buf.data(), buf.size(),
+                          hipMemcpyHostToDevice) != hipSuccess)
                 return BMO_ATTN_READ_ERR_NULL;
         }
         return need;
@@ -478,24 +499,31 @@ void bmo_launch_decode_attention(const float *q_dev, const float *k_dev, const f
     // Mirrors src/bmo_cuda_kernels.cu:850-884: no status is returned, so
     // rejected arguments launch nothing (as an invalid launch would) and are
     // reported on stderr once.
+    static bool warned = false;
+    auto reject = [](const char *why) {
+        if (!warned) {
+            warned = true;
+            std::fprintf(stderr, "[bmo_attn] bmo_launch_decode_attention: %s\n", why);
+        }
+    };
     if (!q_dev || !k_dev || !v_dev || !k_cache_dev || !v_cache_dev || !out_dev ||
         (head_dim != 64 && head_dim != 128) || n_heads <= 0 || n_kv_heads <= 0 ||
         n_heads % n_kv_heads != 0 || n_ctx <= 0 || n_ctx > 65536 || layer < 0 ||
-        (pos_dev == nullptr && n_past < 0)) {
-        static bool warned = false;
-        if (!warned) {
-            warned = true;
-            std::fprintf(stderr, "[bmo_attn] bmo_launch_decode_attention: invalid arguments\n");
-        }
-        return;
-    }
+        (pos_dev == nullptr && n_past < 0))
+        return reject("invalid arguments");
+    // Both cache pointers address the one ring allocation.
+    if (static_cast<uint8_t *>(v_cache_dev) != static_cast<uint8_t *>(k_cache_dev) + bmo::kVCodeOff)
+        return reject("v_cache_dev must be bmo_kv_ring_v_base of the ring whose k_base is k_cache_dev");
     bmo::DecodeParams p{};
     // The reference cache has n_heads head slots per layer and one session.
     p.g = bmo::make_geom(layer + 1, 1, n_heads, head_dim, n_ctx);
-    p.k_base = static_cast<const uint8_t *>(k_cache_dev);
-    p.v_base = static_cast<const uint8_t *>(v_cache_dev);
-    p.k_wbase = static_cast<uint8_t *>(k_cache_dev);
-    p.v_wbase = static_cast<uint8_t *>(v_cache_dev);
+    if (bmo_kv_ring_t *r = registry_find(k_cache_dev)) {
+        const bmo::RingGeom &rg = r->g;
+        if (rg.head_dim != head_dim || rg.n_ctx != n_ctx || rg.n_sessions != 1 ||
+            rg.n_kv_heads != n_heads || layer >= rg.n_layers)
+            return reject("arguments do not match the ring's geometry");
+    }
+    p.base = static_cast<uint8_t *>(k_cache_dev);
     p.layer = layer;
     p.n_batch = 1;
     p.n_heads = n_heads;

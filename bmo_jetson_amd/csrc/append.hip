@@ -11,6 +11,8 @@
 // a 2-byte scale.  The traffic is 2 * n_kv_heads * head_dim * 4 bytes in per
 // row, so this kernel is small next to the attention read; it is written for
 // exactness, with coalescing left to the cache.
+#include <algorithm>
+
 #include "kernels.hpp"
 #include "q4_0_device.hpp"
 
@@ -47,8 +49,32 @@ __global__ __launch_bounds__(256) void append_kernel(AppendParams p) {
     uint16_t d16;
     uint32_t qs[4];
     quantize_block_q4_0(x, d16, qs);
-    uint8_t *stripe = (which == 0 ? p.k_base : p.v_base) + p.g.stripe_offset(p.layer, session, h);
-    store_block(stripe, p.g, slot, blk, d16, qs);
+    store_block(p.base + p.g.stripe_offset(p.layer, session, h), p.g, slot, blk, which, d16, qs);
+}
+
+// Zero state of the ring (ring_layout.hpp): K code bytes 0x88, the rest 0.
+// blockIdx.y selects the range; ranges are whole groups.
+__global__ __launch_bounds__(256) void clear_kernel(uint8_t *base, int64_t range_bytes,
+                                                    int64_t range_stride) {
+    uint4 *dst = reinterpret_cast<uint4 *>(base + (int64_t) blockIdx.y * range_stride);
+    const int64_t n = range_bytes / 16;
+    constexpr int per_group = kGroupBytes / 16;
+    constexpr int k_codes = kVCodeOff / 16;
+    const uint32_t kz = 0x01010101u * kKCodeZero;
+    for (int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t) gridDim.x * blockDim.x) {
+        const uint32_t w = (int) (i % per_group) < k_codes ? kz : 0u;
+        dst[i] = make_uint4(w, w, w, w);
+    }
+}
+
+void launch_clear(uint8_t *base, int64_t range_bytes, int64_t range_stride, int n_ranges,
+                  hipStream_t stream) {
+    if (range_bytes <= 0 || n_ranges <= 0) return;
+    const int64_t vecs = range_bytes / 16;
+    const unsigned gx = (unsigned) std::min<int64_t>((vecs + 255) / 256, 8192);
+    hipLaunchKernelGGL(clear_kernel, dim3(gx, (unsigned) n_ranges), dim3(256), 0, stream, base,
+                       range_bytes, range_stride);
 }
 
 void launch_append(const AppendParams &p, hipStream_t stream) {

@@ -10,49 +10,54 @@
 // position 0, afterwards it is the whole ring), and softmax does not depend on
 // key order, so keys are visited in slot order.
 //
-// Work decomposition (gfx950, wave64): one workgroup of NW waves per (batch
-// entry, query head).  Lane (kk, blk) of a wave owns block blk of key kk of
-// an iteration: LPK = head_dim/32 lanes per key, KPI = 64/LPK keys per wave
-// iteration.  One 128-bit load per lane fetches a whole block's 16 code bytes,
-// so each wave load instruction reads KPI consecutive key rows (1 KiB) of the
-// nibble plane; scales come from the fp16 scale plane as one coalesced 2-byte
-// load per lane.  Waves take iterations round-robin, TIT iterations per tile;
-// the loads of the next PF tiles are in flight while a tile is computed.  Loads
-// are unconditional (slots clamped into the ring); keys outside the window
-// (and, fused, the slot being written) get score -inf and weight 0 by select,
-// so stale bytes never reach the sums.
+// Work decomposition (gfx950, wave64).  A workgroup of NW waves serves one
+// (batch entry, query head) unit; its waves take contiguous pieces of the
+// window.  Batches with many units use one wave per unit; small batches (B=1
+// decode) use up to 16 waves per unit so that enough waves run, merging in LDS
+// (a split across workgroups would have to merge through device-scope
+// atomics, which serialize across the XCDs).  The ring stores slots in groups
+// of G = 64 / LPK keys
+// (ring_layout.hpp), LPK = head_dim / 32 blocks per key, so one group is one
+// wave iteration: lane l owns block l % LPK of key l / LPK and fetches its 16
+// K code bytes, 16 V code bytes and its (K, V) scale dword with three
+// coalesced loads from the group's 2304 contiguous bytes.  The loads are
+// nontemporal: every ring byte is read once per step and the working set is
+// far larger than the caches.  Each wave walks a contiguous run of groups,
+// keeping the loads of the next PF groups in flight while one group is
+// computed.  Keys past the window (and, fused, the slot being written) get
+// weight 0 by select.
 //
-// K side (q . k), two forms:
-//   KDOT8: the lane's 32 query values are turned once into 20-bit fixed point,
-//     U_e = round(q_e / sq) + 2^19, held as five nibble planes laid out like
-//     the code dwords; v_dot8_u32_u4 then multiplies 8 codes by 8 query
-//     nibbles per instruction:  sum_e c_e U_e = sum_i 16^i sum_e c_e u_ei,
-//     and sum_e (c_e - 8) q_e = sq (sum_e c_e U_e - 2^19 sum_e c_e - 8 sum_e Q_e).
-//     Quantizing q costs at most sq/2 = max|q| / (2^20 - 2) per element.
-//   fma-mix: masking a code dword with 0x000F000F (0x00F000F0) leaves two
-//     fp16 subnormals equal to c * 2^-24 (c * 2^-20); v_fma_mix_f32 reads them
-//     next to the fp32 query pre-scaled by 2^24 (2^20):
-//     sum_e (c_e - 8) d q_e = d (sum_e c_e q_e - 8 sum_e q_e).
-// V side: the same fma-mix form accumulates sum_i (p_i d_i) c_ie, and
-// 8 sum_i p_i d_i is subtracted at the end.  q is pre-multiplied by
-// scale * log2(e) so the softmax uses exp2.
+// K side: q (times scale * log2 e) is turned once per wave into 16-bit fixed
+// point per 32-element block, Q_e = round(q_e / sq), |Q_e| <= 30583, and
+// written as four planes of signed base-16 digits, Q_e = sum_i 16^i s_ie with
+// s_ie in [-8, 7], laid out like the code dwords.  The ring keeps K codes as
+// signed nibbles c_e - 8, so v_dot8_i32_i4 gives
+//   sum_e (c_e - 8) Q_e = sum_i 16^i sum_e (c_e - 8) s_ie
+// in 16 instructions per block, exactly, with no correction terms; the block
+// score is that integer times sq times the block scale.  Fixed point costs at
+// most sq / 2 = max|q| / 61166 per query element.
 //
-// Each lane keeps a running (max, sum, acc[32]) over its keys (online softmax,
-// rescaled only when some lane's max rose); at the end every lane is brought
-// to the wave max, the lanes of each 16-lane row that share a block are summed
-// by DPP rotations, the row sums go to LDS, and the first head_dim threads
-// merge waves and rows.
+// V side: masking a code dword with 0x000F000F (0x00F000F0) leaves two fp16
+// subnormals equal to c * 2^-24 (c * 2^-20); v_fma_mix_f32 reads them next to
+// the fp32 weight p * d pre-scaled by 2^24 (2^20) and accumulates
+// sum_i p_i d_i c_ie in fp32; 8 sum_i p_i d_i is subtracted at the end.
+//
+// Softmax is online per lane (running max m, sum l, acc[32]).  A lane
+// rescales only when a score exceeds its running max by more than 8 (log2
+// units), so weights stay below 2^8 and rescaling is rare after the first
+// keys; the result does not depend on the threshold.  At the end every lane
+// is brought to the wave max, lanes sharing a block are summed by DPP
+// rotations, rows go through LDS and the workgroup's threads merge waves.
 //
 // Fused append (the reference's write-then-attend,
 // src/bmo_cuda_kernels.cu:749-754): the current token's K/V rows are quantized
-// in registers with the bit-exact quantizer, wave 0 attends to that key from
+// in registers with the bit-exact quantizer (the K blocks by lanes 0..LPK-1,
+// the V blocks by the next LPK lanes), wave 0 attends to that key from
 // registers, and the first query head of each kv group stores the blocks to
 // slot pos % n_ctx.  Every workgroup masks that slot out of its ring reads.
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
-
-#include <type_traits>
 
 #include "kernels.hpp"
 #include "q4_0_device.hpp"
@@ -65,7 +70,9 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
 constexpr float kTwo24 = 16777216.0f;
 constexpr float kTwo20 = 1048576.0f;
-constexpr int kQFix = 524287;  // 2^19 - 1: largest |Q| of the fixed-point query
+constexpr int kQMax = 30583;      // 7 * (1 + 16 + 256 + 4096): largest |Q|
+constexpr int kQBias = 34952;     // 8 * (1 + 16 + 256 + 4096)
+constexpr float kRescale = 8.0f;  // lazy rescale threshold, log2 units
 
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
@@ -101,114 +108,63 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
-// Element of the block held by nibble k (0..7, from bit 0) of code dword c:
-// dword c holds code bytes 4c..4c+3, byte j has element j in its low and
-// element j+16 in its high nibble.
-__host__ __device__ constexpr int nibble_element(int c, int k) { return 4 * c + (k >> 1) + 16 * (k & 1); }
+// K-side scorer: sum_e (c_e - 8) q_e of one block, before the block scale.
+struct Scorer {
+    uint32_t dig[4][4];  // signed digit plane i, laid out like code dword c
+    float sq;            // fixed-point step of this lane's block
 
-// Element read by operand slot s (0..7) of code dword c in the fma-mix
-// operand order (A.x, A.y, B.x, B.y, C.x, C.y, D.x, D.y) with
-// A = w & 0x000F000F, B = w & 0x00F000F0, C = (w >> 8) & 0x000F000F,
-// D = (w >> 8) & 0x00F000F0.
-__host__ __device__ constexpr int mix_slot_element(int c, int s) {
-    return 4 * c + ((s >> 2) & 1) + 2 * (s & 1) + 16 * ((s >> 1) & 1);
+    // w4: the block's 16 K code bytes as stored (signed nibbles c - 8).
+    __device__ __forceinline__ float operator()(const uint4 &w4) const {
+        const int w[4] = {(int) w4.x, (int) w4.y, (int) w4.z, (int) w4.w};
+        int a = 0;
+#pragma unroll
+        for (int i = 3; i >= 0; --i) {
+            if (i != 3) a <<= 4;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) a = __builtin_amdgcn_sdot8(w[c], (int) dig[i][c], a, false);
+        }
+        return (float) a * sq;
+    }
+};
+
+// One wave turns the query row of its unit into the Scorer digit planes of
+// every block: lane l makes dword c = l % 4 of plane i = (l / 4) % 4 of block
+// (l / 16) % LPK, which holds the digits of elements 4c..4c+3 (low nibbles)
+// and 4c+16..4c+19 (high nibbles).  Results go to this wave's LDS slice.
+template <int D>
+__device__ __forceinline__ void prep_digits(const float *__restrict__ qrow, float qscale, int lane,
+                                            uint32_t *s_dig, float *s_sq) {
+    constexpr int LPK = D / kQK;
+    const int blk = (lane >> 4) % LPK;
+    const int i = (lane >> 2) & 3;
+    const int c = lane & 3;
+    const float4 lo = *reinterpret_cast<const float4 *>(qrow + blk * kQK + 4 * c);
+    const float4 hi = *reinterpret_cast<const float4 *>(qrow + blk * kQK + 4 * c + 16);
+    const float x[8] = {lo.x * qscale, lo.y * qscale, lo.z * qscale, lo.w * qscale,
+                        hi.x * qscale, hi.y * qscale, hi.z * qscale, hi.w * qscale};
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) amax = fmaxf(amax, __builtin_fabsf(x[j]));
+    amax = fmaxf(amax, dpp<0xB1>(amax));  // the four lanes c = 0..3 of this block
+    amax = fmaxf(amax, dpp<0x4E>(amax));
+    const float inv = amax > 0.0f ? (float) kQMax / amax : 0.0f;
+    uint32_t dw = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        int Q = (int) __builtin_rintf(x[j] * inv);
+        Q = min(max(Q, -kQMax), kQMax);
+        const uint32_t digit = ((((uint32_t) (Q + kQBias)) >> (4 * i)) & 15u) ^ 8u;
+        const int nib = (j < 4) ? 2 * j : 2 * (j - 4) + 1;
+        dw |= digit << (4 * nib);
+    }
+    if (lane < 16 * LPK) {
+        s_dig[lane] = dw;
+        if ((lane & 15) == 0) s_sq[blk] = amax * (1.0f / (float) kQMax);
+    }
 }
 
-// K-side scorer over fp32 queries: sum_e (c_e - 8) q_e of one block, before
-// the block scale.
-struct MixScorer {
-    float qm[32];  // query in fma-mix operand order, scaled by 2^24 / 2^20
-    float qsum;
-
-    __device__ __forceinline__ void init(const float (&qe)[32]) {
-        qsum = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 32; ++e) qsum += qe[e];
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-#pragma unroll
-            for (int s = 0; s < 8; ++s) {
-                const int e = mix_slot_element(c, s);
-                qm[8 * c + s] = qe[e] * ((e >= 16) ? kTwo20 : kTwo24);
-            }
-    }
-    __device__ __forceinline__ float operator()(const uint4 &w4) const {
-        const uint32_t w[4] = {w4.x, w4.y, w4.z, w4.w};
-        float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const uint32_t w8 = w[c] >> 8;
-            const half2_t A = __builtin_bit_cast(half2_t, w[c] & 0x000F000Fu);
-            const half2_t B = __builtin_bit_cast(half2_t, w[c] & 0x00F000F0u);
-            const half2_t C = __builtin_bit_cast(half2_t, w8 & 0x000F000Fu);
-            const half2_t D = __builtin_bit_cast(half2_t, w8 & 0x00F000F0u);
-            a0 = __builtin_fmaf((float) A.x, qm[8 * c + 0], a0);
-            a1 = __builtin_fmaf((float) A.y, qm[8 * c + 1], a1);
-            a0 = __builtin_fmaf((float) B.x, qm[8 * c + 2], a0);
-            a1 = __builtin_fmaf((float) B.y, qm[8 * c + 3], a1);
-            a0 = __builtin_fmaf((float) C.x, qm[8 * c + 4], a0);
-            a1 = __builtin_fmaf((float) C.y, qm[8 * c + 5], a1);
-            a0 = __builtin_fmaf((float) D.x, qm[8 * c + 6], a0);
-            a1 = __builtin_fmaf((float) D.y, qm[8 * c + 7], a1);
-        }
-        return (a0 + a1) - 8.0f * qsum;
-    }
-};
-
-// K-side scorer over the 20-bit fixed-point query (v_dot8_u32_u4).
-struct Dot8Scorer {
-    uint32_t dig[5][4];  // nibble plane i of U, laid out like code dword c
-    int bias;            // 8 * sum_e Q_e
-    float sq;            // fixed-point step of the query
-
-    __device__ __forceinline__ void init(const float (&qe)[32]) {
-        float amax = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 32; ++e) amax = fmaxf(amax, __builtin_fabsf(qe[e]));
-        const float inv = amax > 0.0f ? (float) kQFix / amax : 0.0f;
-        sq = amax * (1.0f / (float) kQFix);
-        int qs = 0;
-        uint32_t u[32];
-#pragma unroll
-        for (int e = 0; e < 32; ++e) {
-            int Q = (int) __builtin_rintf(qe[e] * inv);
-            Q = min(max(Q, -kQFix), kQFix);
-            qs += Q;
-            u[e] = (uint32_t) (Q + kQFix + 1);
-        }
-        bias = 8 * qs;
-#pragma unroll
-        for (int i = 0; i < 5; ++i)
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                uint32_t d = 0;
-#pragma unroll
-                for (int k = 0; k < 8; ++k) d |= ((u[nibble_element(c, k)] >> (4 * i)) & 15u) << (4 * k);
-                dig[i][c] = d;
-            }
-    }
-    __device__ __forceinline__ float operator()(const uint4 &w4) const {
-        const uint32_t w[4] = {w4.x, w4.y, w4.z, w4.w};
-        uint32_t S[5];
-#pragma unroll
-        for (int i = 0; i < 5; ++i) {
-            uint32_t a = __builtin_amdgcn_udot8(w[0], dig[i][0], 0u, false);
-            a = __builtin_amdgcn_udot8(w[1], dig[i][1], a, false);
-            a = __builtin_amdgcn_udot8(w[2], dig[i][2], a, false);
-            S[i] = __builtin_amdgcn_udot8(w[3], dig[i][3], a, false);
-        }
-        uint32_t n = __builtin_amdgcn_udot8(w[0], 0x11111111u, 0u, false);
-        n = __builtin_amdgcn_udot8(w[1], 0x11111111u, n, false);
-        n = __builtin_amdgcn_udot8(w[2], 0x11111111u, n, false);
-        n = __builtin_amdgcn_udot8(w[3], 0x11111111u, n, false);
-        // sum_e c_e U_e - 2^19 sum_e c_e - 8 sum_e Q_e, exact in 32-bit integers
-        const uint32_t t = S[0] + (S[1] << 4) + (S[2] << 8) + (S[3] << 12) + (S[4] << 16);
-        const int T = (int) (t - (n << 19)) - bias;
-        return (float) T * sq;
-    }
-};
-
-// acc[e] += pd * c_e for the 32 elements of one block (acc in element order).
+// acc[e] += pd * c_e for the 32 elements of one block (acc in element order;
+// w4 holds plain codes 0..15).
 __device__ __forceinline__ void block_axpy(const uint4 &w4, float pd, float (&acc)[32]) {
     const uint32_t w[4] = {w4.x, w4.y, w4.z, w4.w};
     const float pl = pd * kTwo24;
@@ -219,30 +175,32 @@ __device__ __forceinline__ void block_axpy(const uint4 &w4, float pd, float (&ac
         const half2_t A = __builtin_bit_cast(half2_t, w[c] & 0x000F000Fu);
         const half2_t B = __builtin_bit_cast(half2_t, w[c] & 0x00F000F0u);
         const half2_t C = __builtin_bit_cast(half2_t, w8 & 0x000F000Fu);
-        const half2_t D = __builtin_bit_cast(half2_t, w8 & 0x00F000F0u);
+        const half2_t E = __builtin_bit_cast(half2_t, w8 & 0x00F000F0u);
         acc[4 * c + 0] = __builtin_fmaf((float) A.x, pl, acc[4 * c + 0]);
         acc[4 * c + 2] = __builtin_fmaf((float) A.y, pl, acc[4 * c + 2]);
         acc[4 * c + 16] = __builtin_fmaf((float) B.x, ph, acc[4 * c + 16]);
         acc[4 * c + 18] = __builtin_fmaf((float) B.y, ph, acc[4 * c + 18]);
         acc[4 * c + 1] = __builtin_fmaf((float) C.x, pl, acc[4 * c + 1]);
         acc[4 * c + 3] = __builtin_fmaf((float) C.y, pl, acc[4 * c + 3]);
-        acc[4 * c + 17] = __builtin_fmaf((float) D.x, ph, acc[4 * c + 17]);
-        acc[4 * c + 19] = __builtin_fmaf((float) D.y, ph, acc[4 * c + 19]);
+        acc[4 * c + 17] = __builtin_fmaf((float) E.x, ph, acc[4 * c + 17]);
+        acc[4 * c + 19] = __builtin_fmaf((float) E.y, ph, acc[4 * c + 19]);
     }
 }
 
 }  // namespace
 
-template <int D, int NW, int TIT, int PF, bool KDOT8, bool FUSED>
+template <int D, int NW, int PF, bool FUSED>
 __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
-    constexpr int LPK = D / kQK;   // lanes (blocks) per key row
-    constexpr int KPI = 64 / LPK;  // keys per wave iteration
+    constexpr int LPK = D / kQK;   // lanes (blocks) per key
+    constexpr int G = 64 / LPK;    // keys per group = per wave iteration
     constexpr int ROWS = 4;        // 16-lane rows per wave
-    using Scorer = typename std::conditional<KDOT8, Dot8Scorer, MixScorer>::type;
+    constexpr int NB = PF + 1;     // resident groups per wave
 
-    __shared__ float s_acc[NW * ROWS * D];
+    __shared__ __align__(16) float s_acc[NW * ROWS * D];
+    __shared__ __align__(16) uint32_t s_dig[NW][64];
     __shared__ float s_m[NW];
     __shared__ float s_l[NW];
+    __shared__ float s_sq[NW][4];
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -263,66 +221,46 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     }
     const int q_per_kv = p.n_heads / p.n_kv;
     const int kvh = h / q_per_kv;
-    const int n_ctx = g.n_ctx;
-    const int window = (int) min((int64_t) pos + 1, (int64_t) n_ctx);
-    const int cur = pos % n_ctx;
+    const int window = (int) min((int64_t) pos + 1, (int64_t) g.n_ctx);
+    const int cur = pos % g.n_ctx;
+    uint8_t *stripe = p.base + g.stripe_offset(p.layer, sid, kvh);
 
-    const int64_t soff = g.stripe_offset(p.layer, sid, kvh);
-    const uint8_t *knib = p.k_base + soff;
-    const uint8_t *vnib = p.v_base + soff;
-    const uint8_t *kscl = knib + g.nib_bytes;
-    const uint8_t *vscl = vnib + g.nib_bytes;
+    // Contiguous group run of this wave.
+    const int n_grp = (window + G - 1) / G;
+    const int g0 = wave * n_grp / NW;
+    const int n_it = (wave + 1) * n_grp / NW - g0;
 
-    // Tiles: wave w visits the global iterations (t*TIT + i)*NW + w,
-    // t = 0, 1, ...; a tile is TIT such iterations.  NB tiles are resident: the
-    // loads of the next NB-1 tiles are in flight while one is computed.  The
-    // first tiles' loads are issued before the query preparation so that it
-    // overlaps their latency.
-    constexpr int NB = PF + 1;
-    const int n_iter = (window + KPI - 1) / KPI;
-    const int n_tiles = (n_iter - wave + NW * TIT - 1) / (NW * TIT);
-    const int last_slot = n_ctx - 1;
-    struct Tile {
-        uint4 kq[TIT], vq[TIT];
-        uint32_t ksc[TIT], vsc[TIT];
+    struct Grp {
+        uint4 k, v;
+        uint32_t sc;
     };
-    auto slot_of = [&](int t, int i) { return ((t * TIT + i) * NW + wave) * KPI + kk; };
-    auto slot_ok = [&](int slot) {
-        bool ok = slot < window;
-        if constexpr (FUSED) ok = ok && slot != cur;
-        return ok;
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    auto load = [&](int it, Grp &T) {
+        const uint8_t *gp = stripe + (int64_t) (g0 + it) * kGroupBytes;
+        const u32x4 kc = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(gp + lane * 16));
+        const u32x4 vc =
+            __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(gp + kVCodeOff + lane * 16));
+        T.k = make_uint4(kc.x, kc.y, kc.z, kc.w);
+        T.v = make_uint4(vc.x, vc.y, vc.z, vc.w);
+        T.sc = __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(gp + kScaleOff + lane * 4));
     };
-    auto load_tile = [&](int t, Tile &T) {
-#pragma unroll
-        for (int i = 0; i < TIT; ++i) {
-            const uint32_t slot = (uint32_t) min(slot_of(t, i), last_slot);
-            const uint32_t on = slot * (uint32_t) (D / 2) + (uint32_t) blk * 16u;
-            const uint32_t os = (slot * (uint32_t) LPK + (uint32_t) blk) * 2u;
-            T.kq[i] = *reinterpret_cast<const uint4 *>(knib + on);
-            T.vq[i] = *reinterpret_cast<const uint4 *>(vnib + on);
-            T.ksc[i] = *reinterpret_cast<const uint16_t *>(kscl + os);
-            T.vsc[i] = *reinterpret_cast<const uint16_t *>(vscl + os);
-        }
-    };
-    Tile buf[NB];
+    Grp buf[NB];
 #pragma unroll
     for (int j = 0; j < NB - 1; ++j)
-        if (j < n_tiles) load_tile(j, buf[j]);
+        if (j < n_it) load(j, buf[j]);
 
+    prep_digits<D>(p.q + (int64_t) unit * D, p.qscale, lane, s_dig[wave], s_sq[wave]);
+    __syncthreads();
     Scorer score;
-    {
-        const float4 *q4 = reinterpret_cast<const float4 *>(p.q + (int64_t) unit * D + blk * kQK);
-        float qe[32];
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            const float4 t = q4[c];
-            qe[4 * c + 0] = t.x * p.qscale;
-            qe[4 * c + 1] = t.y * p.qscale;
-            qe[4 * c + 2] = t.z * p.qscale;
-            qe[4 * c + 3] = t.w * p.qscale;
-        }
-        score.init(qe);
+    for (int i = 0; i < 4; ++i) {
+        const uint4 d4 = *reinterpret_cast<const uint4 *>(&s_dig[wave][blk * 16 + i * 4]);
+        score.dig[i][0] = d4.x;
+        score.dig[i][1] = d4.y;
+        score.dig[i][2] = d4.z;
+        score.dig[i][3] = d4.w;
     }
+    score.sq = s_sq[wave][blk];
 
     float m = -INFINITY;  // running max of this lane's keys (log2 domain)
     float l = 0.0f;       // running sum of this lane's keys (each key counted LPK times)
@@ -333,73 +271,71 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
 
     if constexpr (FUSED) {
         if (wave == 0) {
-            // The current token's K and V blocks: lanes 0..LPK-1 (kk == 0) own
-            // block blk of the kv head's new rows.
-            float s_new = 0.0f;
-            uint4 vq_new = make_uint4(0, 0, 0, 0);
-            float vd_new = 0.0f;
-            if (kk == 0) {
-                const int64_t row = ((int64_t) b * p.n_kv + kvh) * D + blk * kQK;
+            // The current token's blocks: lane blk (kk == 0) quantizes K block
+            // blk, lane LPK + blk (kk == 1) V block blk; the V codes and scale
+            // then move to lane blk, which attends to the new key.
+            uint32_t qs[4] = {0u, 0u, 0u, 0u};
+            uint32_t d16 = 0;
+            if (kk < 2) {
+                const float *src = (kk == 0 ? p.k_new : p.v_new) +
+                                   ((int64_t) b * p.n_kv + kvh) * D + blk * kQK;
                 float x[kQK];
-                uint16_t kd16, vd16;
-                uint32_t kqs[4], vqs[4];
-                load_block_f32(p.k_new + row, x);
-                quantize_block_q4_0(x, kd16, kqs);
-                load_block_f32(p.v_new + row, x);
-                quantize_block_q4_0(x, vd16, vqs);
-                vq_new = make_uint4(vqs[0], vqs[1], vqs[2], vqs[3]);
-                s_new = f16_bits_to_f32(kd16) * score(make_uint4(kqs[0], kqs[1], kqs[2], kqs[3]));
-                vd_new = f16_bits_to_f32(vd16);
-                if (h % q_per_kv == 0) {
-                    store_block(p.k_wbase + soff, g, cur, blk, kd16, kqs);
-                    store_block(p.v_wbase + soff, g, cur, blk, vd16, vqs);
-                }
+                load_block_f32(src, x);
+                uint16_t d;
+                quantize_block_q4_0(x, d, qs);
+                d16 = d;
+                if (h % q_per_kv == 0) store_block(stripe, g, cur, blk, kk, d, qs);
+            }
+            // lane blk receives lane LPK + blk's V block
+            uint32_t vq[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) vq[c] = (uint32_t) __shfl((int) qs[c], lane + LPK);
+            const uint32_t vd16 = (uint32_t) __shfl((int) d16, lane + LPK);
+            float s_new = 0.0f;
+            if (kk == 0) {
+                const uint4 kflip = make_uint4(qs[0] ^ 0x88888888u, qs[1] ^ 0x88888888u,
+                                               qs[2] ^ 0x88888888u, qs[3] ^ 0x88888888u);
+                s_new = f16_bits_to_f32(d16) * score(kflip);
             }
             s_new = key_sum<LPK>(s_new);
             if (kk == 0) {
+                const float vd_new = f16_bits_to_f32(vd16);
                 m = s_new;
                 l = 1.0f;  // exp2(s_new - m)
                 csum = vd_new;
-                block_axpy(vq_new, vd_new, acc);
+                block_axpy(make_uint4(vq[0], vq[1], vq[2], vq[3]), vd_new, acc);
             }
         }
     }
 
-    auto compute_tile = [&](int t, const Tile &T) {
-        float s[TIT];
-        float tmax = m;
-#pragma unroll
-        for (int i = 0; i < TIT; ++i) {
-            const float sk = key_sum<LPK>(f16_bits_to_f32(T.ksc[i]) * score(T.kq[i]));
-            s[i] = slot_ok(slot_of(t, i)) ? sk : -INFINITY;
-            tmax = fmaxf(tmax, s[i]);
-        }
-        if (__any(tmax > m)) {
-            float alpha = 1.0f;
-            if (tmax > m) alpha = (m == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m - tmax);
-            m = tmax;
+    auto compute = [&](int it, const Grp &T) {
+        const int slot = (g0 + it) * G + kk;
+        bool ok = slot < window;
+        if constexpr (FUSED) ok = ok && slot != cur;
+        const float sk = key_sum<LPK>(f16_bits_to_f32(T.sc & 0xFFFFu) * score(T.k));
+        const float s = ok ? sk : -INFINITY;
+        const bool need = s > m + kRescale;
+        if (__any(need)) {
+            const float alpha = need ? ((m == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m - s)) : 1.0f;
+            m = need ? s : m;
             l *= alpha;
             csum *= alpha;
 #pragma unroll
             for (int e = 0; e < 32; ++e) acc[e] *= alpha;
         }
-#pragma unroll
-        for (int i = 0; i < TIT; ++i) {
-            const bool ok = s[i] != -INFINITY;
-            const float pk = ok ? __builtin_amdgcn_exp2f(s[i] - m) : 0.0f;
-            l += pk;
-            const float pd = ok ? pk * f16_bits_to_f32(T.vsc[i]) : 0.0f;
-            csum += pd;
-            block_axpy(T.vq[i], pd, acc);
-        }
+        const float pk = ok ? __builtin_amdgcn_exp2f(s - m) : 0.0f;
+        l += pk;
+        const float pd = pk * f16_bits_to_f32(T.sc >> 16);
+        csum += pd;
+        block_axpy(T.v, pd, acc);
     };
-    for (int t = 0; t < n_tiles; t += NB) {
+    for (int t = 0; t < n_it; t += NB) {
 #pragma unroll
         for (int u = 0; u < NB; ++u) {
             const int tt = t + u;
-            if (tt < n_tiles) {
-                if (tt + NB - 1 < n_tiles) load_tile(tt + NB - 1, buf[(u + NB - 1) % NB]);
-                compute_tile(tt, buf[u]);
+            if (tt < n_it) {
+                if (tt + NB - 1 < n_it) load(tt + NB - 1, buf[(u + NB - 1) % NB]);
+                compute(tt, buf[u]);
             }
         }
     }
@@ -435,73 +371,97 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
 #pragma unroll
     for (int w = 1; w < NW; ++w) M = fmaxf(M, s_m[w]);
     float fw[NW];
-    float L = 0.0f;
+    float L = 0.0f;  // sum of weights of the whole window
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
         fw[w] = (s_m[w] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(s_m[w] - M);
         L = __builtin_fmaf(fw[w], s_l[w], L);
     }
-    const float inv_l = (L > 0.0f) ? 1.0f / L : 0.0f;
-    for (int o = threadIdx.x; o < D; o += 64 * NW) {
-        float acc_o = 0.0f;
+    // Thread t sums the rows of waves w = t / D (mod the number of row
+    // groups) for output t % D; row groups beyond the first add through LDS.
+    constexpr int TPB = 64 * NW;
+    constexpr int NPART = TPB >= D ? TPB / D : 1;       // partial sums per output
+    constexpr int WPP = (NW + NPART - 1) / NPART;       // waves per partial
+    constexpr int PER_T = TPB >= D ? 1 : D / TPB;       // outputs per thread
+    float part[PER_T];
 #pragma unroll
-        for (int w = 0; w < NW; ++w) {
-            float r = 0.0f;
+    for (int j = 0; j < PER_T; ++j) {
+        const int o = (threadIdx.x + j * TPB) % D;
+        const int pp = TPB >= D ? threadIdx.x / D : 0;
+        float a = 0.0f;
 #pragma unroll
-            for (int rr = 0; rr < ROWS; ++rr) r += s_acc[(w * ROWS + rr) * D + o];
-            acc_o = __builtin_fmaf(fw[w], r, acc_o);
+        for (int ww = 0; ww < WPP; ++ww) {
+            const int w = pp * WPP + ww;
+            if (w < NW) {
+                float r = 0.0f;
+#pragma unroll
+                for (int rr = 0; rr < ROWS; ++rr) r += s_acc[(w * ROWS + rr) * D + o];
+                a = __builtin_fmaf(fw[w], r, a);
+            }
         }
-        out_row[o] = acc_o * inv_l;
+        part[j] = a;
+    }
+    const float inv_l = (L > 0.0f) ? 1.0f / L : 0.0f;
+    if constexpr (NPART == 1) {
+#pragma unroll
+        for (int j = 0; j < PER_T; ++j) out_row[threadIdx.x + j * TPB] = part[0 + j] * inv_l;
+    } else {
+        __syncthreads();  // every thread has read s_acc; reuse it for the partials
+        s_acc[threadIdx.x] = part[0];
+        __syncthreads();
+        if (threadIdx.x < D) {
+            float a = 0.0f;
+#pragma unroll
+            for (int pp = 0; pp < NPART; ++pp) a += s_acc[pp * D + threadIdx.x];
+            out_row[threadIdx.x] = a * inv_l;
+        }
     }
 }
 
 namespace {
 
-template <int D, int NW, int TIT, int PF, bool KDOT8>
+template <int D, int NW, int PF>
 void launch_variant(const DecodeParams &p, bool fused, hipStream_t stream) {
     const dim3 grid((unsigned) ((int64_t) p.n_batch * p.n_heads)), block(64 * NW);
     if (fused)
-        hipLaunchKernelGGL((decode_kernel<D, NW, TIT, PF, KDOT8, true>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((decode_kernel<D, NW, PF, true>), grid, block, 0, stream, p);
     else
-        hipLaunchKernelGGL((decode_kernel<D, NW, TIT, PF, KDOT8, false>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((decode_kernel<D, NW, PF, false>), grid, block, 0, stream, p);
 }
 
 struct Shape {
-    int nw, tit, pf, kdot8;
+    int nw, pf;
 };
 
-// Workgroup shape per call.  Few (entry, head) units: 4 waves per unit so the
-// window streams with enough loads in flight, fp32 queries (no per-wave query
-// preparation on the latency path).  Many units: one wave per unit walking the
-// whole window with double-buffered tiles and the fixed-point K scorer, whose
-// one-time preparation is spread over the window.  BMO_ATTN_SHAPE =
-// "nw,tit,pf,kdot8" overrides the choice (tuning; unknown shapes fall back).
+// Workgroup shape per call: one wave per (entry, head) unit when there are
+// enough units to fill the chip, else enough waves per unit for about 512
+// waves in all.  BMO_ATTN_SHAPE = "nw,pf" overrides the choice (tuning;
+// unknown shapes fall back to the default).
 Shape pick_shape(int64_t units) {
-    Shape s = units < 512 ? Shape{4, 4, 0, 0} : Shape{1, 4, 1, 1};
+    Shape s{1, 1};
+    if (units < 128) s = Shape{16, 1};
+    else if (units < 256) s = Shape{4, 1};
+    else if (units < 512) s = Shape{2, 1};
     if (const char *e = std::getenv("BMO_ATTN_SHAPE")) {
-        Shape o{0, 0, 0, 0};
-        if (std::sscanf(e, "%d,%d,%d,%d", &o.nw, &o.tit, &o.pf, &o.kdot8) == 4) s = o;
+        Shape o{0, 0};
+        if (std::sscanf(e, "%d,%d", &o.nw, &o.pf) == 2) s = o;
     }
     return s;
 }
 
 template <int D>
 bool launch_shape(const DecodeParams &p, bool fused, hipStream_t stream, const Shape &s) {
-#define BMO_SHAPE(NW_, TIT_, PF_, K8_)                                   \
-    if (s.nw == NW_ && s.tit == TIT_ && s.pf == PF_ && s.kdot8 == K8_) { \
-        launch_variant<D, NW_, TIT_, PF_, K8_>(p, fused, stream);        \
-        return true;                                                     \
+#define BMO_SHAPE(NW_, PF_)                                \
+    if (s.nw == NW_ && s.pf == PF_) {                      \
+        launch_variant<D, NW_, PF_>(p, fused, stream);     \
+        return true;                                       \
     }
-    BMO_SHAPE(4, 4, 0, 0)
-    BMO_SHAPE(4, 2, 1, 0)
-    BMO_SHAPE(4, 4, 1, 0)
-    BMO_SHAPE(1, 4, 1, 1)
-    BMO_SHAPE(1, 4, 2, 1)
-    BMO_SHAPE(1, 2, 2, 1)
-    BMO_SHAPE(1, 2, 3, 1)
-    BMO_SHAPE(1, 8, 1, 1)
-    BMO_SHAPE(2, 4, 1, 1)
-    BMO_SHAPE(2, 2, 2, 1)
+    BMO_SHAPE(1, 1)
+    BMO_SHAPE(1, 2)
+    BMO_SHAPE(2, 1)
+    BMO_SHAPE(4, 1)
+    BMO_SHAPE(8, 1)
+    BMO_SHAPE(16, 1)
 #undef BMO_SHAPE
     return false;
 }
@@ -513,10 +473,9 @@ bool launch_decode(const DecodeParams &p, bool fused, hipStream_t stream) {
     if (units <= 0) return true;
     const Shape s = pick_shape(units);
     if (p.g.head_dim == 128) {
-        if (!launch_shape<128>(p, fused, stream, s))
-            launch_variant<128, 4, 4, 0, false>(p, fused, stream);
+        if (!launch_shape<128>(p, fused, stream, s)) launch_variant<128, 1, 1>(p, fused, stream);
     } else if (p.g.head_dim == 64) {
-        if (!launch_shape<64>(p, fused, stream, s)) launch_variant<64, 4, 4, 0, false>(p, fused, stream);
+        if (!launch_shape<64>(p, fused, stream, s)) launch_variant<64, 1, 1>(p, fused, stream);
     } else {
         return false;
     }

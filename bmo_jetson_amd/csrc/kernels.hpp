@@ -15,8 +15,7 @@ namespace bmo {
 //   run mode (pos == nullptr):          session `session`,
 //                                       slot (pos0 + r) % n_ctx.
 struct AppendParams {
-    uint8_t *k_base;
-    uint8_t *v_base;
+    uint8_t *base;  // ring allocation (layout in ring_layout.hpp)
     RingGeom g;
     int layer;
     int n_rows;
@@ -29,10 +28,7 @@ struct AppendParams {
 };
 
 struct DecodeParams {
-    const uint8_t *k_base;
-    const uint8_t *v_base;
-    uint8_t *k_wbase;  // fused append target (== k_base)
-    uint8_t *v_wbase;
+    uint8_t *base;  // ring allocation; the fused path writes the current slot
     RingGeom g;
     int layer;
     int n_batch;
@@ -43,7 +39,7 @@ struct DecodeParams {
     const int *pos;          // device [n_batch], or nullptr -> pos_scalar
     int pos_scalar;
     const float *q;      // [n_batch][n_heads][head_dim]
-    const float *k_new;  // [n_batch][n_kv_heads][head_dim] (fused only)
+    const float *k_new;  // [n_batch][n_kv][head_dim] (fused only)
     const float *v_new;
     float *out;          // [n_batch][n_heads][head_dim]
     float qscale;        // softmax scale * log2(e)
@@ -53,5 +49,9 @@ struct DecodeParams {
 // hipGetLastError().  launch_decode returns false for an unsupported head_dim.
 void launch_append(const AppendParams &p, hipStream_t stream);
 bool launch_decode(const DecodeParams &p, bool fused, hipStream_t stream);
+// Writes the zero state (ring_layout.hpp) into n_ranges ranges of
+// range_bytes bytes (a multiple of the group size) spaced range_stride apart.
+void launch_clear(uint8_t *base, int64_t range_bytes, int64_t range_stride, int n_ranges,
+                  hipStream_t stream);
 
 }  // namespace bmo

@@ -92,14 +92,18 @@ __device__ __forceinline__ void load_block_f32(const float *__restrict__ src, fl
     }
 }
 
-// Stores a quantized block at slot `slot`, block `blk` of a ring stripe.
+// Stores a quantized block of K (which == 0) or V (which == 1) at slot
+// `slot`, block `blk` of a ring stripe (layout in ring_layout.hpp: K codes
+// are stored as code ^ 8, the scale goes to its half of the slot's scale
+// dword).
 __device__ __forceinline__ void store_block(uint8_t *__restrict__ stripe, const RingGeom &g,
-                                            int slot, int blk, uint16_t d16,
+                                            int slot, int blk, int which, uint16_t d16,
                                             const uint32_t (&qs)[4]) {
-    uint4 *nib = reinterpret_cast<uint4 *>(stripe + (int64_t) slot * (g.head_dim / 2) + blk * 16);
-    *nib = make_uint4(qs[0], qs[1], qs[2], qs[3]);
-    uint16_t *sc = reinterpret_cast<uint16_t *>(stripe + g.nib_bytes +
-                                                ((int64_t) slot * (g.head_dim / kQK) + blk) * 2);
+    const uint32_t flip = which == 0 ? 0x88888888u : 0u;
+    uint4 *codes = reinterpret_cast<uint4 *>(
+        stripe + (which == 0 ? g.kcode_offset(slot, blk) : g.vcode_offset(slot, blk)));
+    *codes = make_uint4(qs[0] ^ flip, qs[1] ^ flip, qs[2] ^ flip, qs[3] ^ flip);
+    uint16_t *sc = reinterpret_cast<uint16_t *>(stripe + g.scale_offset(slot, blk)) + which;
     *sc = d16;
 }
 

@@ -14,9 +14,11 @@
  *   - Plain C types only.  Device pointers are HIP device addresses, streams
  *     are hipStream_t passed as void* (NULL = the null stream), exactly as the
  *     reference passes cudaStream_t as void*.
- *   - Every call is asynchronous on its stream unless it says otherwise.  Calls
- *     on one ring must be ordered on one stream: the ring owns one split-merge
- *     workspace, and two calls on one ring that overlap in time race on it.
+ *   - Every call is asynchronous on its stream unless it says otherwise.  A
+ *     call that writes slots (append, fused append+decode, write, reset,
+ *     import) must be ordered with the calls that read those slots, as on one
+ *     stream; decode calls alone may overlap.  No call allocates device
+ *     memory except bmo_kv_ring_create.
  *   - Functions returning int return BMO_ATTN_OK (0) or an error code below;
  *     bmo_kv_ring_last_error() then describes the most recent failure on that
  *     ring (as bmo_last_error does per handle, src/bmo_api.h:145).
@@ -26,11 +28,15 @@
  *     Appends quantize bit-exactly as ggml quantize_row_q4_0_ref.
  *
  * Ring layout in HBM (what the kernels read; export/import convert to and
- * from ggml's 18-byte AoS blocks):
- *   two regions, K and V, each [n_layers][n_sessions][n_kv_heads] stripes of
- *   bmo_kv_ring_stripe_bytes(head_dim, n_ctx) bytes; a stripe holds the
- *   nibble plane [n_ctx][head_dim/2] bytes followed by the scale plane
- *   [n_ctx][head_dim/32] fp16.  Slot of absolute position p is p % n_ctx.
+ * from ggml's 18-byte AoS blocks): one allocation of
+ *   [n_layers][n_sessions][n_kv_heads] stripes of
+ * bmo_kv_ring_stripe_bytes(head_dim, n_ctx) bytes.  A stripe holds the
+ * n_ctx slots of one kv head in groups of G = 2048/head_dim slots; a group
+ * is 2304 bytes: K codes [G][head_dim/2] (stored as code ^ 8 per nibble),
+ * V codes [G][head_dim/2], then one dword per (slot, block) holding the K
+ * scale (fp16, low half) and the V scale (high half).  Slot of absolute
+ * position p is p % n_ctx.  A fresh or reset slot holds the ggml block with
+ * d = 0 and all codes 0.
  */
 #ifndef BMO_ATTN_H
 #define BMO_ATTN_H
@@ -65,7 +71,8 @@ typedef struct bmo_kv_ring bmo_kv_ring_t;
 
 /* ---- allocation (replaces bmo_init_kv_cache, src/bmo.cpp:1348-1508) ------- */
 
-/* Bytes of one (layer, session, kv head) stripe of K (or of V). */
+/* Bytes of one (layer, session, kv head) stripe (its K and V); 0 for an
+ * unsupported head_dim or n_ctx <= 0. */
 BMO_ATTN_API int64_t bmo_kv_ring_stripe_bytes(int head_dim, int n_ctx);
 
 /* Allocates and zeroes a ring on the current HIP device.  head_dim must be 64
@@ -87,7 +94,9 @@ BMO_ATTN_API int bmo_kv_ring_geometry(const bmo_kv_ring_t *ring, int *n_layers,
                                       int *head_dim, int *n_ctx);
 BMO_ATTN_API int64_t bmo_kv_ring_bytes(const bmo_kv_ring_t *ring);
 
-/* Base addresses of the K and V regions, for bmo_launch_decode_attention. */
+/* The two cache pointers bmo_launch_decode_attention takes for this ring:
+ * k_base is the ring allocation, v_base = k_base + 1024 (the V codes' offset
+ * inside a slot group).  They are not separate regions. */
 BMO_ATTN_API void *bmo_kv_ring_k_base(bmo_kv_ring_t *ring);
 BMO_ATTN_API void *bmo_kv_ring_v_base(bmo_kv_ring_t *ring);
 
@@ -194,8 +203,11 @@ BMO_ATTN_API int64_t bmo_kv_ring_import_q4_0(bmo_kv_ring_t *ring, int layer,
  * pos = *pos_dev when pos_dev is non-NULL, else n_past.  k_cache_dev and
  * v_cache_dev are bmo_kv_ring_k_base / bmo_kv_ring_v_base of a ring created
  * with n_sessions == 1 and n_kv_heads == n_heads (the reference allocates
- * n_heads head slots, src/bmo.cpp:1401-1402).  Returns nothing, as the
- * reference does; launch errors surface through hipGetLastError(). */
+ * n_heads head slots, src/bmo.cpp:1401-1402).  When k_cache_dev is a ring
+ * from bmo_kv_ring_create its geometry is checked; arguments that do not fit
+ * launch nothing and are reported once on stderr.
+ * Returns nothing, as the reference does; launch errors surface through
+ * hipGetLastError(). */
 BMO_ATTN_API void bmo_launch_decode_attention(
     const float *q_dev, const float *k_dev, const float *v_dev,
     void *k_cache_dev, void *v_cache_dev, float *out_dev, int head_dim,

@@ -30,11 +30,15 @@ def test_header_symbols_exported():
 
 def test_stripe_bytes():
     L = bmo.lib()
-    # temporal: 512 slots * (64 code bytes + 8 scale bytes) = 36864 (a 256 multiple)
-    assert L.bmo_kv_ring_stripe_bytes(128, 512) == 512 * 72
-    # depformer: 8 * 36 = 288 -> padded to 512
-    assert L.bmo_kv_ring_stripe_bytes(64, 8) == 512
+    # K and V of one kv head: groups of 2048/head_dim slots, 2304 bytes each
+    # (K codes, V codes, one (K, V) scale dword per block).
+    # temporal: 512 slots = 32 groups of 16 = 512 * (64 + 64 + 16) bytes
+    assert L.bmo_kv_ring_stripe_bytes(128, 512) == 512 * 144 == 32 * 2304
+    # depformer: 8 slots fit one group of 32 (slots 8..31 are padding)
+    assert L.bmo_kv_ring_stripe_bytes(64, 8) == 2304
+    assert L.bmo_kv_ring_stripe_bytes(128, 17) == 2 * 2304
     assert L.bmo_kv_ring_stripe_bytes(0, 8) == 0
+    assert L.bmo_kv_ring_stripe_bytes(96, 8) == 0
 
 
 @pytest.mark.parametrize("args", [(0, 1, 1, 128, 8), (1, 0, 1, 128, 8), (1, 1, 0, 128, 8),
@@ -69,7 +73,9 @@ def test_node_launcher_rejects_bad_arguments_without_launching():
     bmo.launch_decode_attention(None, None, None, None, None, None, 128, 32, 32, 512, 0, 0)
     # unsupported head_dim with non-NULL (never dereferenced) addresses
     fake = 0x1000
-    bmo.launch_decode_attention(fake, fake, fake, fake, fake, fake, 96, 32, 32, 512, 0, 0)
+    bmo.launch_decode_attention(fake, fake, fake, fake, fake + 1024, fake, 96, 32, 32, 512, 0, 0)
+    # v_cache must be k_cache + 1024 (the V codes' offset inside a slot group)
+    bmo.launch_decode_attention(fake, fake, fake, fake, fake + 4096, fake, 128, 32, 32, 512, 0, 0)
 
 
 def test_package_fails_loudly_without_library(tmp_path, monkeypatch):

@@ -316,20 +316,20 @@ def test_api_errors_on_device(gpu):
     ring.decode(0, pos, x, x, 4)  # a good call clears the message
     assert ring.last_error() is None
     assert ring.geometry() == (2, 2, 4, 128, 16)
-    assert ring.nbytes == 2 * (2 * 2 * 4) * stripe_bytes(128, 16)
+    assert ring.nbytes == (2 * 2 * 4) * stripe_bytes(128, 16)
 
 
-# every shape compiled into launch_shape() (decode.hip)
-SHAPES = ["4,4,0,0", "4,2,1,0", "4,4,1,0", "1,4,1,1", "1,4,2,1", "1,2,2,1", "1,2,3,1", "1,8,1,1",
-          "2,4,1,1", "2,2,2,1"]
+# every (waves per unit, prefetch depth) shape compiled into launch_shape()
+# (decode.hip)
+SHAPES = ["1,1", "1,2", "2,1", "4,1", "8,1", "16,1"]
 
 
 @pytest.mark.parametrize("shape", SHAPES)
 @pytest.mark.parametrize("d,n_ctx,pos", [(128, 512, 700), (128, 512, 130), (64, 8, 5), (64, 200, 450)])
 @pytest.mark.parametrize("fused", [False, True])
 def test_every_workgroup_shape(gpu, monkeypatch, shape, d, n_ctx, pos, fused):
-    """Each compiled workgroup shape (waves, tile, prefetch depth, K scorer),
-    forced through BMO_ATTN_SHAPE, against the oracle."""
+    """Each compiled workgroup shape (waves per unit, prefetch depth), forced
+    through BMO_ATTN_SHAPE, against the oracle."""
     monkeypatch.setenv("BMO_ATTN_SHAPE", shape)
     n_sess, n_heads, n_kv = 3, 8, 4
     m = Mirror(gpu, 1, n_sess, n_kv, d, n_ctx)
@@ -359,8 +359,8 @@ def test_every_workgroup_shape(gpu, monkeypatch, shape, d, n_ctx, pos, fused):
 
 @pytest.mark.parametrize("fused", [False, True])
 def test_large_batch_default_shape(gpu, fused):
-    """>= 512 (entry, head) units selects the batch shape (one wave per unit,
-    fixed-point K scorer): 64 sessions x 8 heads, random wrap points."""
+    """>= 512 (entry, head) units selects the batch shape (one wave per unit):
+    64 sessions x 8 heads, random wrap points."""
     n_sess, n_heads, d, n_ctx = 64, 8, 128, 128
     m = Mirror(gpu, 2, n_sess, n_heads, d, n_ctx)
     rng = np.random.default_rng(5)
@@ -388,3 +388,29 @@ def test_large_batch_default_shape(gpu, fused):
     if fused:
         for s in range(0, n_sess, 7):
             m.assert_ring_equal(layer, s)
+
+
+def test_b1_repeated_calls(gpu):
+    """B=1 calls (16 waves per head merging in LDS): a run of calls at
+    changing positions (full windows, wraps, fused and plain) on one ring."""
+    n_heads, d, n_ctx = 32, 128, 512
+    m = Mirror(gpu, 1, 1, n_heads, d, n_ctx)
+    m.fill_range(0, 0, 0, 600, seed=77)
+    out = gpu.full((n_heads * d,), float("nan"), dtype=gpu.float32, device="cuda")
+    p = 600
+    for step in range(6):
+        q = oracle.normal(800 + step, n_heads * d)
+        if step % 2:
+            k = oracle.normal(900 + step, n_heads * d)
+            v = oracle.normal(950 + step, n_heads * d)
+            m.ring.append_decode(0, _i32(gpu, [p]), m.dev(q), m.dev(k), m.dev(v), out, n_heads,
+                                 stream=m.stream)
+            m.oracle_append(0, 0, p, k, v)
+        else:
+            m.ring.decode(0, _i32(gpu, [p - 1]), m.dev(q), out, n_heads, stream=m.stream)
+        gpu.cuda.synchronize()
+        ref = m.oracle_decode(0, 0, p if step % 2 else p - 1, q, n_heads)
+        check_close(out.cpu().numpy().reshape(n_heads, d), ref, f"step {step}")
+        if step % 2:
+            p += 1
+    m.assert_ring_equal(0, 0)
