@@ -48,6 +48,21 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
+def read_traffic(config):
+    """HBM bytes per launch of the dominant kernel, from the committed
+    rocprofv3 PMC summary (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by the
+    copy-kernel calibration), or None when there is none for this workload."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        f"decode_{config}_traffic.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1].strip())
+    except OSError:
+        pass
+    return None
+
+
 def fill_ring(torch, ring, L, S, H, D, W, pos_host, seed, outlier_p=0.01):
     gen = torch.Generator(device="cuda")
     gen.manual_seed(seed)
@@ -66,27 +81,82 @@ def fill_ring(torch, ring, L, S, H, D, W, pos_host, seed, outlier_p=0.01):
     torch.cuda.synchronize()
 
 
-def time_steps(torch, step, steps, warmup, per_launch_events):
-    """Runs warmup steps, then times exactly `steps` steps between two
-    synchronizations.  step(ev) launches one step; when ev is a list it records
-    an event pair around every launch on the launch stream."""
-    for _ in range(warmup):
-        step(None)
+def capture_graph(torch, launch):
+    """Captures launch(stream) into a HIP graph on a side stream."""
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            launch(torch.cuda.current_stream())
+    torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
-    pairs = [] if per_launch_events else None
+    return graph
+
+
+def time_steps(torch, launch_layer, n_layers, steps, warmup):
+    """Runs `warmup` eager steps, then two timed regions of exactly `steps`
+    steps each, every region bracketed by torch.cuda.synchronize():
+      A. the step (n_layers launches) replayed from a HIP graph, timed by one
+         event pair around the region: the step time;
+      B. the same steps launched eagerly with a HIP event pair recorded on the
+         launch stream around every launch: per-launch kernel durations.
+    Returns (ms per step from A, mean ms per launch from B, ms per step from B)."""
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        for layer in range(n_layers):
+            launch_layer(layer, stream)
+    torch.cuda.synchronize()
+
+    def whole_step(st):
+        for layer in range(n_layers):
+            launch_layer(layer, st)
+
+    graph = capture_graph(torch, whole_step)
+    graph.replay()
+    torch.cuda.synchronize()
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0.record()
+    t0.record(stream)
     for _ in range(steps):
-        step(pairs)
-    t1.record()
+        graph.replay()
+    t1.record(stream)
     torch.cuda.synchronize()
-    ms = t0.elapsed_time(t1)
-    launch_ms = None
-    if pairs:
-        launch_ms = float(np.mean([a.elapsed_time(b) for a, b in pairs]))
-    return ms, launch_ms
+    ms_graph = t0.elapsed_time(t1) / steps
+    del graph
+
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(steps * n_layers)]
+    torch.cuda.synchronize()
+    t0.record(stream)
+    i = 0
+    for _ in range(steps):
+        for layer in range(n_layers):
+            a, b = evs[i]
+            a.record(stream)
+            launch_layer(layer, stream)
+            b.record(stream)
+            i += 1
+    t1.record(stream)
+    torch.cuda.synchronize()
+    launch_ms = float(np.mean([a.elapsed_time(b) for a, b in evs]))
+    return ms_graph, launch_ms, t0.elapsed_time(t1) / steps
+
+
+def graph_us_per_call(torch, call, calls_per_graph, reps=5):
+    """Microseconds per call from HIP-graph replays of calls_per_graph calls."""
+    graph = capture_graph(torch, lambda st: [call(st) for _ in range(calls_per_graph)])
+    graph.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    del graph
+    return e0.elapsed_time(e1) * 1000.0 / (reps * calls_per_graph)
 
 
 def bench_b1(torch, iters=200):
@@ -108,44 +178,24 @@ def bench_b1(torch, iters=200):
     v = torch.randn(H * D, device="cuda", generator=g)
     out = torch.empty(H * D, device="cuda")
     res = {}
-    for name, fn in (
-        ("fused", lambda: ring.append_decode(0, pos, q, k, v, out, H, stream=stream)),
-        ("decode", lambda: ring.decode(0, pos, q, out, H, stream=stream)),
-    ):
+    calls = {
+        "fused": lambda st: ring.append_decode(0, pos, q, k, v, out, H, stream=st),
+        "decode": lambda st: ring.decode(0, pos, q, out, H, stream=st),
+    }
+    for name, fn in calls.items():
         for _ in range(20):
-            fn()
+            fn(stream)
         torch.cuda.synchronize()
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         e0.record()
         for _ in range(iters):
-            fn()
+            fn(stream)
         e1.record()
         torch.cuda.synchronize()
         eager_us = e0.elapsed_time(e1) * 1000.0 / iters
-        graph = torch.cuda.CUDAGraph()
-        s = torch.cuda.Stream()
-        s.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(s):
-            stream_cap = torch.cuda.current_stream()
-            with torch.cuda.graph(graph, stream=s):
-                for _ in range(iters):
-                    if name == "fused":
-                        ring.append_decode(0, pos, q, k, v, out, H, stream=stream_cap)
-                    else:
-                        ring.decode(0, pos, q, out, H, stream=stream_cap)
-        torch.cuda.current_stream().wait_stream(s)
-        graph.replay()
-        torch.cuda.synchronize()
-        reps = 5
-        e0.record()
-        for _ in range(reps):
-            graph.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        graph_us = e0.elapsed_time(e1) * 1000.0 / (reps * iters)
-        res[name] = {"graph_us": round(graph_us, 3), "eager_us": round(eager_us, 3)}
-        del graph
+        res[name] = {"graph_us": round(graph_us_per_call(torch, fn, iters), 3),
+                     "eager_us": round(eager_us, 3)}
     ring.close()
     b = unit_bytes(H, D, W)
     return {
@@ -156,6 +206,50 @@ def bench_b1(torch, iters=200):
         "us_per_layer_decode_eager": res["decode"]["eager_us"],
         "decode_GBps_graph": round(b / (res["decode"]["graph_us"] * 1e-6) / 1e9, 1),
         "target_us": 10.0,
+    }
+
+
+def bench_depformer(torch, frames=20):
+    """one depformer frame = the ring reset that
+    bmo_forward_depth_cascade does first (src/bmo_api.cpp:682), then 8
+    codebook steps x 6 layers of fused append+decode (16 heads x head_dim 64,
+    8-slot ring, step s attends to steps 0..s), replayed from a HIP graph."""
+    from bmo_jetson_amd import KVRing
+
+    L, H, D, W, STEPS = 6, 16, 64, 8, 8
+    ring = KVRing(L, 1, H, D, W)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0xB0A00002)
+    q = torch.randn((STEPS, L, H * D), device="cuda", generator=g)
+    k = torch.randn((STEPS, L, H * D), device="cuda", generator=g)
+    v = torch.randn((STEPS, L, H * D), device="cuda", generator=g)
+    out = torch.empty((STEPS, L, H * D), device="cuda")
+    pos = [torch.tensor([s], dtype=torch.int32, device="cuda") for s in range(STEPS)]
+
+    def frame(st):
+        ring.reset(0, stream=st)
+        for s in range(STEPS):
+            for layer in range(L):
+                ring.append_decode(layer, pos[s], q[s, layer], k[s, layer], v[s, layer],
+                                   out[s, layer], H, stream=st)
+
+    stream = torch.cuda.current_stream()
+    for _ in range(3):
+        frame(stream)
+    torch.cuda.synchronize()
+    us_frame = graph_us_per_call(torch, frame, frames)
+    ring.close()
+    # KV read by step s: (s+1) slots x H x 2 x (D/32) x 18 B; q, out fp32; the
+    # appended rows read as fp32 and written as Q4_0.
+    frame_bytes = sum((s + 1) * H * 2 * (D // 32) * 18 for s in range(STEPS)) * L \
+        + STEPS * L * (2 * H * D * 4 + fused_extra_bytes(H, D))
+    return {
+        "workload": "cfg2: depformer L=6 H=16 D=64 W=8, 8 steps per frame, reset + fused "
+                    "append+decode",
+        "us_per_frame_graph": round(us_frame, 3),
+        "us_per_call_graph": round(us_frame / (STEPS * L), 3),
+        "calls_per_frame": STEPS * L,
+        "bytes_per_frame": frame_bytes,
     }
 
 
@@ -267,31 +361,23 @@ def main():
         kn = torch.randn((L, S, H, D), device="cuda", generator=g)
         vn = torch.randn((L, S, H, D), device="cuda", generator=g)
 
-    def step(pairs):
-        for layer in range(L):
-            if pairs is not None:
-                a = torch.cuda.Event(enable_timing=True)
-                b = torch.cuda.Event(enable_timing=True)
-                a.record(stream)
-            if fused:
-                ring.append_decode(layer, pos, q[layer], kn[layer], vn[layer], out[layer], H,
-                                   stream=stream)
-            else:
-                ring.decode(layer, pos, q[layer], out[layer], H, stream=stream)
-            if pairs is not None:
-                b.record(stream)
-                pairs.append((a, b))
+    def launch_layer(layer, st):
+        if fused:
+            ring.append_decode(layer, pos, q[layer], kn[layer], vn[layer], out[layer], H, stream=st)
+        else:
+            ring.decode(layer, pos, q[layer], out[layer], H, stream=st)
 
-    ms, launch_ms = time_steps(torch, step, args.steps, args.warmup, per_launch_events=True)
-    ms_per_step = ms / args.steps
+    ms_per_step, launch_ms, ms_eager = time_steps(torch, launch_layer, L, args.steps, args.warmup)
     per_step_bytes = unit_bytes(H, D, W) * S * L
     if fused:
         per_step_bytes += fused_extra_bytes(H, D) * S * L
     value = per_step_bytes / (ms_per_step * 1e-3) / 1e9
     launch_bytes = per_step_bytes / L
     achieved = launch_bytes / (launch_ms * 1e-3) / 1e9
-    log(f"[bench] {ms_per_step:.3f} ms/step, {value:.1f} GB/s; per launch {launch_ms * 1e3:.2f} us "
-        f"-> {achieved:.1f} GB/s")
+    log(f"[bench] {ms_per_step:.3f} ms/step (graph), {value:.1f} GB/s; per launch "
+        f"{launch_ms * 1e3:.2f} us -> {achieved:.1f} GB/s; eager step {ms_eager:.3f} ms")
+    kernel = "decode_kernel<128, 1, 1, %s>" % ("true" if fused else "false")
+    traffic = read_traffic(args.config)
 
     result = {
         "metric": METRIC,
@@ -315,14 +401,15 @@ def main():
             "parallelism": "none (1 GPU; sessions would shard across GPUs)",
         },
         "hbm_frac": round(value / HBM_PEAK_GBS, 4),
+        "ms_per_step_eager": round(ms_eager, 4),
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "kernel": "decode_kernel<128, %s>" % ("true" if fused else "false"),
+            "traffic": traffic,
+            "kernel": kernel,
             "launch_us": round(launch_ms * 1e3, 3),
             "bytes_per_launch": launch_bytes,
         },
@@ -331,6 +418,8 @@ def main():
     if not args.no_b1:
         result["b1"] = bench_b1(torch)
         log(f"[bench] B=1: {result['b1']}")
+        result["depformer"] = bench_depformer(torch)
+        log(f"[bench] depformer: {result['depformer']}")
     if not args.no_cpu:
         log("[bench] timing the CPU baseline")
         result["cpu_baseline"] = cpu_baseline(torch, ring, L, S, H, D, W, pos_host, q, out,

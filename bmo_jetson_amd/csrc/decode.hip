@@ -244,10 +244,14 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
         T.v = make_uint4(vc.x, vc.y, vc.z, vc.w);
         T.sc = __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(gp + kScaleOff + lane * 4));
     };
+    // Prologue loads are unconditional (a group index past this wave's run
+    // is clamped to the stripe's last group, a harmless in-bounds read), so
+    // the outstanding-load count at the steady-state loop below is the same
+    // on every path and the compiler's wait counts stay exact.
+    auto load_clamped = [&](int it, Grp &T) { load(min(it, g.n_groups - 1 - g0), T); };
     Grp buf[NB];
 #pragma unroll
-    for (int j = 0; j < NB - 1; ++j)
-        if (j < n_it) load(j, buf[j]);
+    for (int j = 0; j < NB - 1; ++j) load_clamped(j, buf[j]);
 
     prep_digits<D>(p.q + (int64_t) unit * D, p.qscale, lane, s_dig[wave], s_sq[wave]);
     __syncthreads();
@@ -329,14 +333,25 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
         csum += pd;
         block_axpy(T.v, pd, acc);
     };
-    for (int t = 0; t < n_it; t += NB) {
+    // Steady state: every load is unconditional, so the wait before a group's
+    // compute is for that group's loads only (a conditional prefetch would
+    // make the compiler wait for the prefetch as well).  buf[u] holds group
+    // t + u at the top of each pass.
+    int t = 0;
+    for (; t + 2 * NB - 2 < n_it; t += NB) {
 #pragma unroll
         for (int u = 0; u < NB; ++u) {
-            const int tt = t + u;
-            if (tt < n_it) {
-                if (tt + NB - 1 < n_it) load(tt + NB - 1, buf[(u + NB - 1) % NB]);
-                compute(tt, buf[u]);
-            }
+            load(t + u + NB - 1, buf[(u + NB - 1) % NB]);
+            compute(t + u, buf[u]);
+        }
+    }
+    // Tail: at most 2 * NB - 2 groups, loads only while groups remain.
+#pragma unroll
+    for (int u = 0; u < 2 * NB - 2; ++u) {
+        const int tt = t + u;
+        if (tt < n_it) {
+            if (tt + NB - 1 < n_it) load(tt + NB - 1, buf[(u + NB - 1) % NB]);
+            compute(tt, buf[u % NB]);
         }
     }
 
@@ -437,11 +452,12 @@ struct Shape {
 // enough units to fill the chip, else enough waves per unit for about 512
 // waves in all.  BMO_ATTN_SHAPE = "nw,pf" overrides the choice (tuning;
 // unknown shapes fall back to the default).
-Shape pick_shape(int64_t units) {
+Shape pick_shape(int64_t units, int n_groups) {
     Shape s{1, 1};
-    if (units < 128) s = Shape{16, 1};
+    if (units < 128) s = Shape{8, 1};
     else if (units < 256) s = Shape{4, 1};
     else if (units < 512) s = Shape{2, 1};
+    while (s.nw > 1 && s.nw > n_groups) s.nw /= 2;  // no more waves than groups
     if (const char *e = std::getenv("BMO_ATTN_SHAPE")) {
         Shape o{0, 0};
         if (std::sscanf(e, "%d,%d", &o.nw, &o.pf) == 2) s = o;
@@ -461,6 +477,7 @@ bool launch_shape(const DecodeParams &p, bool fused, hipStream_t stream, const S
     BMO_SHAPE(2, 1)
     BMO_SHAPE(4, 1)
     BMO_SHAPE(8, 1)
+    BMO_SHAPE(8, 2)
     BMO_SHAPE(16, 1)
 #undef BMO_SHAPE
     return false;
@@ -471,7 +488,7 @@ bool launch_shape(const DecodeParams &p, bool fused, hipStream_t stream, const S
 bool launch_decode(const DecodeParams &p, bool fused, hipStream_t stream) {
     const int64_t units = (int64_t) p.n_batch * p.n_heads;
     if (units <= 0) return true;
-    const Shape s = pick_shape(units);
+    const Shape s = pick_shape(units, p.g.n_groups);
     if (p.g.head_dim == 128) {
         if (!launch_shape<128>(p, fused, stream, s)) launch_variant<128, 1, 1>(p, fused, stream);
     } else if (p.g.head_dim == 64) {
