@@ -13,12 +13,17 @@ of one (session, layer) are the full window's Q4_0 K+V bytes
 (W*H*2*(D/32)*18) plus q and out in fp32 (2*H*D*4): 2,392,064 B, so
 4,898,947,072 B per step.
 
+The step (32 launches, one per layer) is captured in a HIP graph and
+replayed; the timed region is exactly --steps replays between two
+synchronizations, timed by a HIP event pair on the replay stream.  The
+roofline entry divides one launch's algorithmic bytes by the mean launch
+duration from that region (step time / 32, kernel gaps included).
+
 Also reported: B=1 latency (one layer, 32 heads, W=512,
 write head at position 700; fused append+decode as the reference kernel does,
-and decode alone), per-launch durations of the dominant kernel from HIP
-events recorded on the launch stream inside the timed region (roofline), and
-the CPU baseline (the oracle's fp32 restatement of the reference CPU path,
-timed on this host on a bounded sample of the same ring).
+and decode alone), the depformer frame, and the CPU
+baseline (the oracle's fp32 restatement of the reference CPU path, timed on
+this host on a bounded sample of the same ring).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg3|cfg4]
 """
@@ -95,13 +100,12 @@ def capture_graph(torch, launch):
 
 
 def time_steps(torch, launch_layer, n_layers, steps, warmup):
-    """Runs `warmup` eager steps, then two timed regions of exactly `steps`
-    steps each, every region bracketed by torch.cuda.synchronize():
-      A. the step (n_layers launches) replayed from a HIP graph, timed by one
-         event pair around the region: the step time;
-      B. the same steps launched eagerly with a HIP event pair recorded on the
-         launch stream around every launch: per-launch kernel durations.
-    Returns (ms per step from A, mean ms per launch from B, ms per step from B)."""
+    """Runs `warmup` eager steps, captures one step (n_layers launches, one
+    per layer, as the model runs them) into a HIP graph, and times exactly
+    `steps` replays between two torch.cuda.synchronize() calls with a HIP
+    event pair recorded on the replay stream.  Returns ms per step; the mean
+    launch duration is that over n_layers (it includes the small gaps between
+    the graph's kernels, so it is an upper bound on the kernel time)."""
     stream = torch.cuda.current_stream()
     for _ in range(warmup):
         for layer in range(n_layers):
@@ -117,30 +121,14 @@ def time_steps(torch, launch_layer, n_layers, steps, warmup):
     torch.cuda.synchronize()
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
     t0.record(stream)
     for _ in range(steps):
         graph.replay()
     t1.record(stream)
     torch.cuda.synchronize()
-    ms_graph = t0.elapsed_time(t1) / steps
     del graph
-
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(steps * n_layers)]
-    torch.cuda.synchronize()
-    t0.record(stream)
-    i = 0
-    for _ in range(steps):
-        for layer in range(n_layers):
-            a, b = evs[i]
-            a.record(stream)
-            launch_layer(layer, stream)
-            b.record(stream)
-            i += 1
-    t1.record(stream)
-    torch.cuda.synchronize()
-    launch_ms = float(np.mean([a.elapsed_time(b) for a, b in evs]))
-    return ms_graph, launch_ms, t0.elapsed_time(t1) / steps
+    return t0.elapsed_time(t1) / steps
 
 
 def graph_us_per_call(torch, call, calls_per_graph, reps=5):
@@ -367,15 +355,16 @@ def main():
         else:
             ring.decode(layer, pos, q[layer], out[layer], H, stream=st)
 
-    ms_per_step, launch_ms, ms_eager = time_steps(torch, launch_layer, L, args.steps, args.warmup)
+    ms_per_step = time_steps(torch, launch_layer, L, args.steps, args.warmup)
+    launch_ms = ms_per_step / L
     per_step_bytes = unit_bytes(H, D, W) * S * L
     if fused:
         per_step_bytes += fused_extra_bytes(H, D) * S * L
     value = per_step_bytes / (ms_per_step * 1e-3) / 1e9
-    launch_bytes = per_step_bytes / L
+    launch_bytes = per_step_bytes // L
     achieved = launch_bytes / (launch_ms * 1e-3) / 1e9
-    log(f"[bench] {ms_per_step:.3f} ms/step (graph), {value:.1f} GB/s; per launch "
-        f"{launch_ms * 1e3:.2f} us -> {achieved:.1f} GB/s; eager step {ms_eager:.3f} ms")
+    log(f"[bench] {ms_per_step:.3f} ms/step, {value:.1f} GB/s; per launch "
+        f"{launch_ms * 1e3:.2f} us -> {achieved:.1f} GB/s")
     kernel = "decode_kernel<128, 1, 1, %s>" % ("true" if fused else "false")
     traffic = read_traffic(args.config)
 
@@ -401,7 +390,6 @@ def main():
             "parallelism": "none (1 GPU; sessions would shard across GPUs)",
         },
         "hbm_frac": round(value / HBM_PEAK_GBS, 4),
-        "ms_per_step_eager": round(ms_eager, 4),
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 2),
