@@ -26,6 +26,8 @@ struct bmo_kv_ring {
     bmo::RingGeom g{};
     int device = 0;
     uint8_t *mem = nullptr;  // every stripe (layout in ring_layout.hpp)
+    uint8_t *stage = nullptr;  // prefill staging, grown on demand
+    int64_t stage_bytes = 0;
     std::mutex mu;           // guards last_error
     std::string last_error;
 };
@@ -161,6 +163,7 @@ bmo_kv_ring_t *bmo_kv_ring_create(int n_layers, int n_sessions, int n_kv_heads, 
     bmo_kv_ring_t *r = nullptr;
     auto release = [](bmo_kv_ring_t *x) {
         if (x->mem) (void) hipFree(x->mem);
+        if (x->stage) (void) hipFree(x->stage);
         delete x;
     };
     try {
@@ -207,6 +210,7 @@ void bmo_kv_ring_free(bmo_kv_ring_t *ring) {
         }
         DeviceGuard dg(ring->device);
         if (ring->mem) (void) hipFree(ring->mem);
+        if (ring->stage) (void) hipFree(ring->stage);
     } catch (...) {
     }
     delete ring;
@@ -374,6 +378,69 @@ int bmo_kv_ring_write(bmo_kv_ring_t *r, int layer, int session, int64_t pos0, in
         return BMO_ATTN_OK;
     } catch (...) {
         return fail(r, BMO_ATTN_ERR_INTERNAL, "bmo_kv_ring_write: unknown exception");
+    }
+}
+
+int bmo_kv_ring_prefill(bmo_kv_ring_t *r, int layer, int n_batch, const int *session_ids,
+                        const int *pos0, int n_tok, int n_heads, const uint16_t *q,
+                        const uint16_t *k, const uint16_t *v, float *out, float scale,
+                        void *stream) {
+    if (!r) return BMO_ATTN_ERR_NULL;
+    const char *fn = "bmo_kv_ring_prefill";
+    try {
+        if (!pos0 || !q || !k || !v || !out)
+            return fail(r, BMO_ATTN_ERR_NULL, std::string(fn) + ": null pointer argument");
+        if (int rc = check_layer(r, layer, fn)) return rc;
+        if (n_batch <= 0 || n_batch > r->g.n_sessions)
+            return fail(r, BMO_ATTN_ERR_ARG, std::string(fn) + ": n_batch must be in [1, n_sessions]");
+        if (n_tok <= 0 || n_tok > r->g.n_ctx)
+            return fail(r, BMO_ATTN_ERR_ARG, std::string(fn) + ": n_tok must be in [1, n_ctx]");
+        if (n_heads <= 0 || n_heads % r->g.n_kv_heads != 0)
+            return fail(r, BMO_ATTN_ERR_ARG,
+                        std::string(fn) + ": n_heads must be a positive multiple of n_kv_heads");
+        if (!(scale > 0.0f)) scale = 1.0f / std::sqrt((float) r->g.head_dim);
+        if (!std::isfinite(scale))
+            return fail(r, BMO_ATTN_ERR_ARG, std::string(fn) + ": scale must be finite");
+        DeviceGuard dg(r->device);
+        bmo::PrefillParams p{};
+        p.sg = bmo::make_geom(1, n_batch, r->g.n_kv_heads, r->g.head_dim, n_tok);
+        const int64_t need = p.sg.total_bytes();
+        if (need > r->stage_bytes) {
+            // grow-only staging; the previous one may still be read by queued work
+            hipError_t e = hipStreamSynchronize((hipStream_t) stream);
+            if (e == hipSuccess && r->stage) e = hipFree(r->stage);
+            r->stage = nullptr;
+            r->stage_bytes = 0;
+            if (e == hipSuccess) e = hipMalloc(&r->stage, (size_t) need);
+            if (e != hipSuccess) {
+                r->stage = nullptr;
+                return hip_fail(r, e, "bmo_kv_ring_prefill: staging allocation");
+            }
+            r->stage_bytes = need;
+        }
+        p.base = r->mem;
+        p.g = r->g;
+        p.stage = r->stage;
+        p.layer = layer;
+        p.n_batch = n_batch;
+        p.n_heads = n_heads;
+        p.n_kv = r->g.n_kv_heads;
+        p.session_ids = session_ids;
+        p.pos0 = pos0;
+        p.n_tok = n_tok;
+        p.q = q;
+        p.k = k;
+        p.v = v;
+        p.out = out;
+        p.qscale = scale * kLog2e;
+        if (!bmo::launch_prefill(p, (hipStream_t) stream))
+            return fail(r, BMO_ATTN_ERR_ARG, std::string(fn) + ": unsupported head_dim");
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return hip_fail(r, e, fn);
+        clear_error(r);
+        return BMO_ATTN_OK;
+    } catch (...) {
+        return fail(r, BMO_ATTN_ERR_INTERNAL, std::string(fn) + ": unknown exception");
     }
 }
 

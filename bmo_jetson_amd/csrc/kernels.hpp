@@ -45,10 +45,33 @@ struct DecodeParams {
     float qscale;        // softmax scale * log2(e)
 };
 
+// Chunked prefill of n_tok tokens per batch entry (prefill.hip).
+struct PrefillParams {
+    uint8_t *base;  // ring allocation
+    RingGeom g;
+    uint8_t *stage;  // staging stripes [n_batch][n_kv] of n_tok slots
+    RingGeom sg;     // staging geometry (1 layer, n_batch "sessions", n_kv, head_dim, n_tok)
+    int layer;
+    int n_batch;
+    int n_heads;
+    int n_kv;
+    const int *session_ids;  // device, nullable
+    const int *pos0;         // device [n_batch]: position of each entry's first chunk token
+    int n_tok;
+    const uint16_t *q;  // bf16 [n_batch][n_tok][n_heads][head_dim]
+    const uint16_t *k;  // bf16 [n_batch][n_tok][n_kv][head_dim]
+    const uint16_t *v;
+    float *out;    // [n_batch][n_tok][n_heads][head_dim]
+    float qscale;  // softmax scale * log2(e)
+};
+
 // Launchers enqueue only; they leave launch errors for the caller's
 // hipGetLastError().  launch_decode returns false for an unsupported head_dim.
 void launch_append(const AppendParams &p, hipStream_t stream);
 bool launch_decode(const DecodeParams &p, bool fused, hipStream_t stream);
+// stage, attend, commit (three kernels in stream order); false for an
+// unsupported head_dim.
+bool launch_prefill(const PrefillParams &p, hipStream_t stream);
 // Writes the zero state (ring_layout.hpp) into n_ranges ranges of
 // range_bytes bytes (a multiple of the group size) spaced range_stride apart.
 void launch_clear(uint8_t *base, int64_t range_bytes, int64_t range_stride, int n_ranges,

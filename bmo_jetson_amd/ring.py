@@ -145,6 +145,20 @@ class KVRing:
         self._check("bmo_kv_ring_write", lib().bmo_kv_ring_write(
             self._h, layer, session, int(pos0), int(n_tok), _ptr(k), _ptr(v), _stream(stream)))
 
+    def prefill(self, layer: int, pos0, q, k, v, out, n_heads: int, n_tok: int | None = None,
+                session_ids=None, scale: float = 0.0, n_batch=None, stream=None):
+        """Chunked prefill: q [n_batch][n_tok][n_heads][d], k/v
+        [n_batch][n_tok][n_kv][d] as bf16 tensors (or raw bf16 addresses),
+        out [n_batch][n_tok][n_heads][d] fp32; pos0 a device int32 [n_batch]."""
+        n = self._batch(pos0, n_batch)
+        if n_tok is None:
+            n_tok = int(q.shape[-3]) if hasattr(q, "shape") and q.dim() >= 3 else None
+            if n_tok is None:
+                raise ValueError("n_tok is required when q is a raw address")
+        self._check("bmo_kv_ring_prefill", lib().bmo_kv_ring_prefill(
+            self._h, layer, n, _ptr(session_ids), _ptr(pos0), int(n_tok), n_heads, _ptr(q),
+            _ptr(k), _ptr(v), _ptr(out), float(scale), _stream(stream)))
+
     @staticmethod
     def _batch(pos, n_batch):
         if n_batch is not None:

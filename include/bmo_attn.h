@@ -17,8 +17,9 @@
  *   - Every call is asynchronous on its stream unless it says otherwise.  A
  *     call that writes slots (append, fused append+decode, write, reset,
  *     import) must be ordered with the calls that read those slots, as on one
- *     stream; decode calls alone may overlap.  No call allocates device
- *     memory except bmo_kv_ring_create.
+ *     stream; decode calls alone may overlap.  Only bmo_kv_ring_create and
+ *     bmo_kv_ring_prefill (its staging buffer, when a call needs a larger one
+ *     than the ring holds) allocate device memory.
  *   - Functions returning int return BMO_ATTN_OK (0) or an error code below;
  *     bmo_kv_ring_last_error() then describes the most recent failure on that
  *     ring (as bmo_last_error does per handle, src/bmo_api.h:145).
@@ -165,6 +166,31 @@ BMO_ATTN_API int bmo_kv_ring_append_decode(bmo_kv_ring_t *ring, int layer,
 BMO_ATTN_API int bmo_kv_ring_write(bmo_kv_ring_t *ring, int layer, int session,
                                    int64_t pos0, int n_tok, const float *k,
                                    const float *v, void *stream);
+
+/* Chunked prefill (multi-token attention node of the reference's lazy path,
+ * src/bmo_compute.cpp:2376-2418, here over the ring with a causal +
+ * sliding-window mask).  Entry b writes n_tok tokens at positions pos0[b] ..
+ * pos0[b]+n_tok-1 (pos0 a DEVICE array, 1 <= n_tok <= n_ctx) of session
+ * session_ids[b] (or b).  Query i, at position p = pos0[b] + i, attends to
+ * positions max(0, p-n_ctx+1) .. p: those before pos0[b] from the ring as it
+ * stands, chunk positions from the chunk's own K/V quantized to Q4_0 exactly
+ * as bmo_kv_ring_append quantizes them.  Then the chunk's blocks go to slots
+ * (pos0[b]+i) % n_ctx.  The ring must hold the session's positions up to
+ * pos0[b]-1 (or pos0[b] == 0).  Entries with a bad session or pos0 < 0 are
+ * skipped (output zeroed, ring untouched).
+ *   q:    [n_batch][n_tok][n_heads][head_dim] bf16 (bit patterns)
+ *   k, v: [n_batch][n_tok][n_kv_heads][head_dim] bf16
+ *   out:  [n_batch][n_tok][n_heads][head_dim] fp32
+ * Attention runs on matrix cores: K, V and the softmax weights in fp16 (K and
+ * V values must lie in fp16 range, as the reference's F16 cache requires),
+ * q from its bf16 values, fp32 accumulation.  Grows the ring's staging buffer
+ * (n_batch * n_kv_heads stripes of n_tok slots) on first use, with a
+ * synchronization of stream. */
+BMO_ATTN_API int bmo_kv_ring_prefill(bmo_kv_ring_t *ring, int layer, int n_batch,
+                                     const int *session_ids, const int *pos0,
+                                     int n_tok, int n_heads, const uint16_t *q,
+                                     const uint16_t *k, const uint16_t *v,
+                                     float *out, float scale, void *stream);
 
 /* ---- readout / export ------------------------------------------------------- */
 

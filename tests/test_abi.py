@@ -62,6 +62,8 @@ def test_null_handle_paths():
     assert L.bmo_kv_ring_append_decode(None, 0, 1, None, None, 1, None, None, None, None, 0.0,
                                        None) == 1
     assert L.bmo_kv_ring_write(None, 0, 0, 0, 1, None, None, None) == 1
+    assert L.bmo_kv_ring_prefill(None, 0, 1, None, None, 1, 1, None, None, None, None, 0.0,
+                                 None) == 1
     buf = np.zeros(16, np.float32)
     assert L.bmo_kv_ring_copy_k_f32(None, 0, 0, 0, 1, buf.ctypes.data, 16) == -1
     assert L.bmo_kv_ring_export_q4_0(None, 0, 0, 0, 0, 1, buf.ctypes.data, 64) == -1
