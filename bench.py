@@ -241,6 +241,49 @@ def bench_depformer(torch, frames=20):
     }
 
 
+def bench_prefill(torch, reps=10):
+    """chunked prefill of S=16 sessions x C=256 tokens into
+    a W=512 ring, 32 heads x head_dim 128, bf16 q/k/v ~N(0,1), one layer per
+    call (stage + attention + commit), with the ring history full (p0 = 1024)
+    and empty (p0 = 0).  Timed as HIP-graph replays."""
+    from bmo_jetson_amd import KVRing
+
+    S, C, W, H, D = 16, 256, 512, 32, 128
+    res = {"workload": "cfg5: S=16 sessions x C=256 tokens, W=512, H=32, D=128, bf16 q/k/v, "
+                       "causal + window mask; one layer per call"}
+    for name, p0 in (("full", 1024), ("empty", 0)):
+        ring = KVRing(1, S, H, D, W)
+        if p0:
+            fill_ring(torch, ring, 1, S, H, D, W, np.full(S, p0 - 1), 0xB0A00005, outlier_p=0.0)
+        g = torch.Generator(device="cuda")
+        g.manual_seed(0xB0A00005 + p0)
+        q = torch.randn((S, C, H, D), device="cuda", generator=g).to(torch.bfloat16)
+        k = torch.randn((S, C, H, D), device="cuda", generator=g).to(torch.bfloat16)
+        v = torch.randn((S, C, H, D), device="cuda", generator=g).to(torch.bfloat16)
+        out = torch.empty((S, C, H, D), device="cuda")
+        pos0 = torch.full((S,), p0, dtype=torch.int32, device="cuda")
+        call = lambda st: ring.prefill(0, pos0, q, k, v, out, H, n_tok=C, stream=st)
+        for _ in range(3):
+            call(torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        us = graph_us_per_call(torch, call, reps)
+        ring.close()
+        keys = sum(min(p0 + i + 1, W) for i in range(C))  # keys seen per (session, head)
+        flops = 4 * D * keys * H * S
+        # algorithmic bytes: bf16 q/k/v in, fp32 out, the old window read
+        # once (Q4_0), the chunk's Q4_0 blocks written once
+        old = min(p0, W - 1) * H * 2 * (D // 32) * 18 * S
+        qb = S * C * H * D * 2
+        blocks = S * C * H * 2 * (D // 32) * 18
+        bytes_ = 3 * qb + S * C * H * D * 4 + old + blocks
+        res[name] = {"p0": p0, "us_per_layer": round(us, 2), "gflop": round(flops / 1e9, 2),
+                     "tflops": round(flops / (us * 1e-6) / 1e12, 1),
+                     "mfma_frac_of_2500": round(flops / (us * 1e-6) / 2.5e15, 4),
+                     "bytes": bytes_, "GBps": round(bytes_ / (us * 1e-6) / 1e9, 1),
+                     "hbm_frac": round(bytes_ / (us * 1e-6) / 8e12, 4)}
+    return res
+
+
 def cpu_baseline(torch, ring, L, S, H, D, W, pos_host, q_dev, out_dev, budget_s):
     """Times the oracle's fp32 restatement of the reference CPU path
     (src/bmo_compute.cpp:927-970) on host threads over a sample of the same
@@ -408,6 +451,8 @@ def main():
         log(f"[bench] B=1: {result['b1']}")
         result["depformer"] = bench_depformer(torch)
         log(f"[bench] depformer: {result['depformer']}")
+        result["prefill"] = bench_prefill(torch)
+        log(f"[bench] prefill: {result['prefill']}")
     if not args.no_cpu:
         log("[bench] timing the CPU baseline")
         result["cpu_baseline"] = cpu_baseline(torch, ring, L, S, H, D, W, pos_host, q, out,

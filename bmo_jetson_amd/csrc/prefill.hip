@@ -18,13 +18,19 @@
 //   prefill_kernel attention over the ring and the staged chunk;
 //   commit_kernel  copies the staged blocks into their ring slots.
 //
-// prefill_kernel: a workgroup of QW waves serves 16*QW queries of one
-// (entry, head); wave w owns 16 of them.  Keys stream through LDS in tiles of
-// 32 positions: all threads dequantize the tile (K row-major, V transposed)
-// to fp16 value (code - 8) * d, then each wave computes S^T = K Q^T with
+// prefill_kernel: a workgroup of QW waves serves 16*QB*QW queries of one
+// (entry, head); each wave owns QB blocks of 16, so every K and V operand it
+// reads from LDS feeds QB matrix instructions.  Keys stream through two LDS
+// buffers in tiles of 32 positions: every thread fetches its share of the
+// Q4_0 bytes of the tile 3 ahead into registers while the waves compute the
+// current tile, then dequantizes the oldest fetched tile into the free buffer (K and V row-major) as
+// the fp16 value (code - 8) * d; one barrier per tile.  A wave
+// skips tiles that hold no key its queries may see.  Each wave computes
+// S^T = K Q^T with
 // v_mfma_f32_16x16x32_f16 (the D layout of S^T puts 8 keys of one query in a
 // lane, exactly the A layout the P.V product needs), runs an online softmax
-// in the log2 domain and accumulates O += P V with the same instruction.
+// in the log2 domain and accumulates O += P V with the same instruction, its
+// V operand read from the row-major tile with ds_read_b64_tr_b16.
 // Operands: q (bf16 inputs, scaled by scale*log2 e) and the dequantized K, V
 // and the weights P in fp16, accumulation in fp32.  K and V values fit fp16
 // as the reference's F16 cache requires.
@@ -38,6 +44,7 @@ namespace bmo {
 namespace {
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
@@ -48,10 +55,32 @@ __device__ __forceinline__ float bf16_to_f32(uint32_t bits) {
     return __builtin_bit_cast(float, bits << 16);
 }
 
+// ds_read_b64_tr_b16: within each 16-lane group, lanes 4j..4j+3 address 16
+// consecutive halves of some row j (4 each); lane i receives element i of
+// rows 0..3.
+__device__ __forceinline__ half4_t lds_read_tr16(const _Float16 *p) {
+    typedef __fp16 fp16x4 __attribute__((vector_size(8)));
+    typedef __attribute__((address_space(3))) fp16x4 lds_fp16x4;
+    return __builtin_bit_cast(half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_fp16x4 *) p));
+}
+
+// Workgroup barrier for LDS hand-off only: waits for this wave's LDS
+// operations, not for its global loads (__syncthreads' fence would also wait
+// for the loads of the tiles being prefetched).
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // Order of the 8 fp16 values dequantized from code dword c of a block
 // (element 4c + kPerm[r]): the pairs the nibble masks produce.
 __host__ __device__ constexpr int perm_elem(int r) {
     return (r & 4 ? 16 : 0) + (r & 1 ? 2 : 0) + ((r >> 1) & 1);
+}
+
+// Logical element of LDS column s of a dequantized row: slot 8c + r of a
+// block holds element 4c + perm_elem(r).
+__host__ __device__ constexpr int col_elem(int s) {
+    return (s & ~31) + 4 * ((s & 31) >> 3) + perm_elem(s & 7);
 }
 
 // Dequantizes code dword w (plain codes, bytes 4c..4c+3 of a block) with
@@ -140,16 +169,26 @@ __global__ __launch_bounds__(256) void commit_kernel(PrefillParams p) {
         *reinterpret_cast<const uint32_t *>(src + p.sg.scale_offset(i, blk));
 }
 
-template <int D, int QW>
-__global__ __launch_bounds__(64 * QW) void prefill_kernel(PrefillParams p) {
+// Two workgroups per CU: the register budget that keeps the accumulators in
+// architectural registers without spilling.
+template <int D, int QW, int QB>
+__global__ __launch_bounds__(64 * QW, 2) void prefill_kernel(PrefillParams p) {
     constexpr int NBLK = D / kQK;
-    constexpr int KROW = D + 8;    // fp16 per K row in LDS (padded)
-    constexpr int VROW = kTK + 8;  // fp16 per V^T row in LDS (padded)
-    constexpr int QT = 16 * QW;    // queries per workgroup
-    constexpr int NT = D / 16;     // output column tiles per wave
+    // LDS rows (fp16): K rows padded to 68 dwords so that the 16 lanes of an
+    // operand read (16 keys, one 16-byte chunk each) hit 16 distinct 4-bank
+    // slots; V rows padded to 72 dwords so that a transposing read (16 rows,
+    // 8 bytes each) does the same for every 32 lanes.
+    constexpr int KROW = D + 8;
+    constexpr int VROW = D + 16;
+    constexpr int QWV = 16 * QB;   // queries per wave
+    constexpr int QT = QWV * QW;   // queries per workgroup
+    constexpr int NT = D / 16;     // output column tiles
+    // dequantization items per tile: (K/V, key, block, 8-byte half)
+    constexpr int ITEMS = 2 * kTK * NBLK * 2;
+    constexpr int IPT = (ITEMS + 64 * QW - 1) / (64 * QW);
 
-    __shared__ __align__(16) _Float16 sK[kTK * KROW];
-    __shared__ __align__(16) _Float16 sV[D * VROW];
+    __shared__ __align__(16) _Float16 sK[2][kTK * KROW];
+    __shared__ __align__(16) _Float16 sV[2][kTK * VROW];
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -172,161 +211,241 @@ __global__ __launch_bounds__(64 * QW) void prefill_kernel(PrefillParams p) {
         }
         return;
     }
+    // Positions are int: the API bounds them by pos0 + n_tok < 2^31.
     const int n_ctx = p.g.n_ctx;
-    const int64_t p_first = (int64_t) pos0 + i0;
-    const int64_t p_last = (int64_t) pos0 + i0 + nq - 1;
-    const int64_t k_lo = max((int64_t) 0, p_first - n_ctx + 1);
-    const int n_tiles = (int) ((p_last - k_lo) / kTK) + 1;
+    const int p_first = pos0 + i0;
+    const int p_last = pos0 + i0 + nq - 1;
+    const int k_lo = max(0, p_first - n_ctx + 1);
+    const int n_tiles = (p_last - k_lo) / kTK + 1;
+    const int slot0 = pos0 % n_ctx;  // ring slot of position pos0
     const uint8_t *ring = p.base + p.g.stripe_offset(p.layer, sid, kvh);
     const uint8_t *stage = p.stage + p.sg.stripe_offset(0, b, kvh);
+    // Byte offsets inside a stripe (ring_layout.hpp) with the group size
+    // known at compile time.
+    constexpr int G = keys_per_group(D);
+    auto code_off = [](int slot, int bb, int which) {
+        return (slot / G) * kGroupBytes + (slot % G) * (D / 2) + bb * 16 + which * kVCodeOff;
+    };
+    auto scale_off = [](int slot, int bb) {
+        return (slot / G) * kGroupBytes + kScaleOff + ((slot % G) * NBLK + bb) * 4;
+    };
 
-    // Query operand (B of S^T = K Q^T): lane l holds query n = l % 16 of this
-    // wave, block b's values at elements 4c + perm_elem(r), c = l / 16.
+    // Raw tile bytes, fetched PF tiles ahead: this thread's items.  Every
+    // fetch issues its loads (an item past the chunk reads the stripe's slot
+    // 0 and is dequantized with scale 0), so the number of loads in flight
+    // is the same on every path and the compiler's waits stay exact; the
+    // liveness flag is applied at dequantization, not at the load.
+    constexpr int PF = 3;
+    static_assert((PF + 1) % 2 == 0, "LDS buffer parity must follow the unrolled slot");
+    uint2 raw[PF + 1][IPT];
+    uint32_t rawd[PF + 1][IPT];
+    bool rawl[PF + 1][IPT];
+    auto fetch = [&](int tile, uint2 (&rw)[IPT], uint32_t (&rd)[IPT], bool (&rl)[IPT]) {
+        const int t0 = k_lo + tile * kTK;
+#pragma unroll
+        for (int j = 0; j < IPT; ++j) {
+            const int it = min((int) threadIdx.x + j * 64 * QW, ITEMS - 1);
+            const int hf = it & 1;
+            const int bb = (it >> 1) % NBLK;
+            const int key = (it >> 1) / NBLK % kTK;
+            const int which = it / (2 * kTK * NBLK);
+            const int t = t0 + key;
+            const bool live = t <= p_last && (int) threadIdx.x + j * 64 * QW < ITEMS;
+            const bool old = t < pos0;
+            // old position t: slot (slot0 + t - pos0) mod n_ctx, t - pos0 in [-n_ctx, 0)
+            int rslot = slot0 + (t - pos0);
+            rslot += rslot < 0 ? n_ctx : 0;
+            const int slot = !live ? 0 : old ? rslot : t - pos0;
+            const uint8_t *src = old ? ring : stage;
+            rw[j] = *reinterpret_cast<const uint2 *>(src + code_off(slot, bb, which) + 8 * hf);
+            rd[j] = *reinterpret_cast<const uint16_t *>(src + scale_off(slot, bb) + 2 * which);
+            rl[j] = live;
+        }
+    };
+    // Dequantizes fetched items into LDS buffer `buf`: K and V row-major,
+    // the values of code dword cd at slots 8cd..8cd+7 of the block (the order
+    // the query operand uses; col_elem maps a column back to its element).
+    auto deposit = [&](int buf, const uint2 (&rw)[IPT], const uint32_t (&rd)[IPT],
+                       const bool (&rl)[IPT]) {
+#pragma unroll
+        for (int j = 0; j < IPT; ++j) {
+            const int it = threadIdx.x + j * 64 * QW;
+            if (it < ITEMS) {
+                const int hf = it & 1;
+                const int bb = (it >> 1) % NBLK;
+                const int key = (it >> 1) / NBLK % kTK;
+                const int which = it / (2 * kTK * NBLK);
+                const uint32_t flip = which == 0 ? 0x88888888u : 0u;  // K codes are stored as code ^ 8
+                const uint32_t d16 = rl[j] ? rd[j] : 0u;                 // scale 0 past the chunk
+                const half8_t v0 = dequant_dword(rw[j].x ^ flip, d16);
+                const half8_t v1 = dequant_dword(rw[j].y ^ flip, d16);
+                _Float16 *dst = which == 0 ? &sK[buf][key * KROW + bb * kQK + 16 * hf]
+                                           : &sV[buf][key * VROW + bb * kQK + 16 * hf];
+                *reinterpret_cast<half8_t *>(dst) = v0;
+                *reinterpret_cast<half8_t *>(dst + 8) = v1;
+            }
+        }
+    };
+
+    // Query operands (B of S^T = K Q^T): for query block qb lane l holds
+    // query n = l % 16 of that block, block b's values at elements
+    // 4c + perm_elem(r), c = l / 16.  Rows past the chunk read row 0 and are
+    // zeroed.
     const int n = lane & 15;
     const int c = lane >> 4;
-    const int qi = i0 + wave * 16 + n;
-    const bool q_ok = qi < p.n_tok;
-    half8_t qop[NBLK];
-    {
-        const uint16_t *qrow = p.q + (((int64_t) b * p.n_tok + qi) * p.n_heads + h) * D;
+    const int wq0 = i0 + wave * QWV;  // first query of this wave
+    half8_t qop[QB][NBLK];
+    bool q_ok[QB];
+    int pq[QB];  // this lane's query positions (S^T layout)
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+        const int qi = wq0 + qb * 16 + n;
+        q_ok[qb] = qi < p.n_tok;
+        pq[qb] = pos0 + qi;
+        const uint16_t *qrow = p.q + (((int64_t) b * p.n_tok + (q_ok[qb] ? qi : 0)) * p.n_heads + h) * D;
+        uint2 lo[NBLK], hi[NBLK];
 #pragma unroll
         for (int bb = 0; bb < NBLK; ++bb) {
+            lo[bb] = *reinterpret_cast<const uint2 *>(qrow + bb * kQK + 4 * c);
+            hi[bb] = *reinterpret_cast<const uint2 *>(qrow + bb * kQK + 4 * c + 16);
+        }
 #pragma unroll
-            for (int r = 0; r < 8; ++r) {
-                const float x = q_ok ? bf16_to_f32(qrow[bb * kQK + 4 * c + perm_elem(r)]) : 0.0f;
-                qop[bb][r] = (_Float16) (x * p.qscale);
-            }
+        for (int bb = 0; bb < NBLK; ++bb) {
+            // elements 4c + {0,1,2,3} in lo, 4c + 16 + {0,1,2,3} in hi; the
+            // operand order is perm_elem: 0, 2, 1, 3, 16, 18, 17, 19
+            const uint32_t e[8] = {lo[bb].x & 0xFFFFu, lo[bb].y & 0xFFFFu, lo[bb].x >> 16, lo[bb].y >> 16,
+                                   hi[bb].x & 0xFFFFu, hi[bb].y & 0xFFFFu, hi[bb].x >> 16, hi[bb].y >> 16};
+#pragma unroll
+            for (int r = 0; r < 8; ++r)
+                qop[qb][bb][r] = (_Float16) (q_ok[qb] ? bf16_to_f32(e[r]) * p.qscale : 0.0f);
         }
     }
-    const int64_t pq = (int64_t) pos0 + qi;  // this lane's query position (S^T layout)
+    // this wave's query positions and the keys they may see
+    const int wq1 = min(wq0 + QWV - 1, p.n_tok - 1);
+    const int w_hi = pos0 + wq1;
+    const int w_lo = pos0 + wq0 - n_ctx + 1;
 
-    float m = -INFINITY;  // running max of query n (log2 domain)
-    float l = 0.0f;       // this lane's part of query n's weight sum
-    float4_t acc[NT];
+    float m[QB], l[QB];  // running max and this lane's part of the weight sum, per query block
+    float4_t acc[QB][NT];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) acc[t] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int qb = 0; qb < QB; ++qb) {
+        m[qb] = -INFINITY;
+        l[qb] = 0.0f;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[qb][t] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    }
 
-    // Dequantization items: (K/V, key, block, code dword).
-    constexpr int ITEMS = 2 * kTK * NBLK * 4;
-    for (int tile = 0; tile < n_tiles; ++tile) {
-        const int64_t t0 = k_lo + (int64_t) tile * kTK;
-        __syncthreads();  // the previous tile's readers are done
-        for (int it = threadIdx.x; it < ITEMS; it += blockDim.x) {
-            const int cd = it & 3;
-            const int bb = (it >> 2) % NBLK;
-            const int key = (it >> 2) / NBLK % kTK;
-            const int which = it / (kTK * NBLK * 4);
-            const int64_t t = t0 + key;
-            half8_t vals;
-            if (t <= p_last) {
-                const uint8_t *src;
-                int slot;
-                const RingGeom *gg;
-                if (t < pos0) {
-                    src = ring;
-                    slot = (int) (t % n_ctx);
-                    gg = &p.g;
-                } else {
-                    src = stage;
-                    slot = (int) (t - pos0);
-                    gg = &p.sg;
-                }
-                uint32_t w = *reinterpret_cast<const uint32_t *>(
-                    src + (which == 0 ? gg->kcode_offset(slot, bb) : gg->vcode_offset(slot, bb)) +
-                    4 * cd);
-                if (which == 0) w ^= 0x88888888u;  // K codes are stored as code ^ 8
-                const uint32_t d16 =
-                    *reinterpret_cast<const uint16_t *>(src + gg->scale_offset(slot, bb) + 2 * which);
-                vals = dequant_dword(w, d16);
-            } else {
-#pragma unroll
-                for (int r = 0; r < 8; ++r) vals[r] = (_Float16) 0.0f;
-            }
-            if (which == 0) {
-                // K row-major, the 8 values of dword cd at slots 8cd..8cd+7 of
-                // the block (the order the query operand uses)
-                *reinterpret_cast<half8_t *>(&sK[key * KROW + bb * kQK + 8 * cd]) = vals;
-            } else {
-#pragma unroll
-                for (int r = 0; r < 8; ++r) sV[(bb * kQK + 4 * cd + perm_elem(r)) * VROW + key] = vals[r];
-            }
-        }
-        __syncthreads();
-
+    auto compute = [&](int buf, int t0) {
+        if (wq0 >= p.n_tok || t0 > w_hi || t0 + kTK - 1 < w_lo) return;  // nothing to see
         // S^T for keys 0..15 and 16..31 of the tile: lane l gets keys
-        // 4c + v (and 16 + 4c + v) of query n.
-        float4_t s[2];
+        // 4c + v (and 16 + 4c + v) of query n of each query block.
+        float4_t s[QB][2];
 #pragma unroll
         for (int sub = 0; sub < 2; ++sub) {
-            float4_t a = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) s[qb][sub] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int bb = 0; bb < NBLK; ++bb) {
-                const half8_t kop =
-                    *reinterpret_cast<const half8_t *>(&sK[(sub * 16 + n) * KROW + bb * kQK + 8 * c]);
-                a = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop[bb], a, 0, 0, 0);
-            }
-            s[sub] = a;
-        }
-        // mask (causal + window) and tile max of query n
-        float tmax = -INFINITY;
+                const half8_t kop = *reinterpret_cast<const half8_t *>(
+                    &sK[buf][(sub * 16 + n) * KROW + bb * kQK + 8 * c]);
 #pragma unroll
-        for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int64_t t = t0 + sub * 16 + 4 * c + v;
-                const bool ok = q_ok && t <= pq && t > pq - n_ctx;
-                s[sub][v] = ok ? s[sub][v] : -INFINITY;
-                tmax = fmaxf(tmax, s[sub][v]);
-            }
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-        const bool need = tmax > m + kRescale;
-        if (__any(need)) {
-            const float alpha = need ? ((m == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m - tmax)) : 1.0f;
-            m = need ? tmax : m;
-            l *= alpha;
-            // acc rows are queries 4c + v: fetch their alphas from lanes 4c + v
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const float av = __shfl(alpha, 4 * c + v);
-#pragma unroll
-                for (int t = 0; t < NT; ++t) acc[t][v] *= av;
+                for (int qb = 0; qb < QB; ++qb)
+                    s[qb][sub] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop[qb][bb], s[qb][sub], 0, 0, 0);
             }
         }
-        half8_t pop;
+        // mask (causal + window) unless every key of the tile is visible to
+        // every query of the wave
+        const bool whole = wq1 == wq0 + QWV - 1 && t0 + kTK - 1 <= pos0 + wq0 && t0 > w_hi - n_ctx;
+        half8_t pop[QB];
 #pragma unroll
-        for (int sub = 0; sub < 2; ++sub)
+        for (int qb = 0; qb < QB; ++qb) {
+            float tmax = -INFINITY;
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const float pv = (s[sub][v] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(s[sub][v] - m);
-                l += pv;
-                pop[sub * 4 + v] = (_Float16) pv;
+            for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    if (!whole) {
+                        const int t = t0 + sub * 16 + 4 * c + v;
+                        const bool ok = q_ok[qb] && t <= pq[qb] && t > pq[qb] - n_ctx;
+                        s[qb][sub][v] = ok ? s[qb][sub][v] : -INFINITY;
+                    }
+                    tmax = fmaxf(tmax, s[qb][sub][v]);
+                }
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+            const bool need = tmax > m[qb] + kRescale;
+            if (__any(need)) {
+                const float alpha =
+                    need ? ((m[qb] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m[qb] - tmax)) : 1.0f;
+                m[qb] = need ? tmax : m[qb];
+                l[qb] *= alpha;
+                // acc rows are queries 4c + v: fetch their alphas from lanes 4c + v
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const float av = __shfl(alpha, 4 * c + v);
+#pragma unroll
+                    for (int t = 0; t < NT; ++t) acc[qb][t][v] *= av;
+                }
             }
-        // O += P V: B operand lane l = element n of the column tile, keys
-        // 4c..4c+3 and 16+4c..16+4c+3 (the key order of pop)
+#pragma unroll
+            for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const float pv =
+                        (s[qb][sub][v] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(s[qb][sub][v] - m[qb]);
+                    l[qb] += pv;
+                    pop[qb][sub * 4 + v] = (_Float16) pv;
+                }
+        }
+        // O += P V: B operand lane l = column t*16 + n of the tile, keys
+        // 4c..4c+3 and 16+4c..16+4c+3 (the key order of pop), read with two
+        // transposing loads (lane 4j + mm of the group addresses chunk mm of
+        // key row 4c + j, resp. 16 + 4c + j), shared by the query blocks
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            const _Float16 *vrow = &sV[(t * 16 + n) * VROW];
-            const uint2 lo = *reinterpret_cast<const uint2 *>(vrow + 4 * c);
-            const uint2 hi = *reinterpret_cast<const uint2 *>(vrow + 16 + 4 * c);
-            const uint4 vv = make_uint4(lo.x, lo.y, hi.x, hi.y);
-            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pop, __builtin_bit_cast(half8_t, vv), acc[t],
-                                                            0, 0, 0);
+            const _Float16 *vb = &sV[buf][(4 * c + (n >> 2)) * VROW + t * 16 + 4 * (n & 3)];
+            const half4_t lo = lds_read_tr16(vb);
+            const half4_t hi = lds_read_tr16(vb + 16 * VROW);
+            const half8_t vop = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb)
+                acc[qb][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pop[qb], vop, acc[qb][t], 0, 0, 0);
+        }
+    };
+
+    // The trip count is padded to a multiple of PF + 1 tiles (an empty tile
+    // past the chunk is zeros and skipped by every wave), so the unrolled
+    // body has no per-tile condition around its loads.
+#pragma unroll
+    for (int j = 0; j < PF; ++j) fetch(j, raw[j], rawd[j], rawl[j]);
+    for (int base = 0; base < n_tiles; base += PF + 1) {
+#pragma unroll
+        for (int u = 0; u <= PF; ++u) {
+            const int tile = base + u;
+            const int nxt = (u + PF) % (PF + 1);
+            deposit(u & 1, raw[u], rawd[u], rawl[u]);
+            lds_barrier();  // buffer u & 1 is complete; the other is free again
+            fetch(tile + PF, raw[nxt], rawd[nxt], rawl[nxt]);
+            compute(u & 1, k_lo + tile * kTK);
         }
     }
 
     // Row sums of query n, then every acc row (query 4c + v) divides by its own.
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-        const float lv = __shfl(l, 4 * c + v);
-        const int qv = i0 + wave * 16 + 4 * c + v;
-        if (qv < p.n_tok) {
-            float *orow = p.out + (((int64_t) b * p.n_tok + qv) * p.n_heads + h) * D;
-            const float inv = lv > 0.0f ? 1.0f / lv : 0.0f;
+    for (int qb = 0; qb < QB; ++qb) {
+        float lq = l[qb];
+        lq += __shfl_xor(lq, 16);
+        lq += __shfl_xor(lq, 32);
 #pragma unroll
-            for (int t = 0; t < NT; ++t) orow[t * 16 + n] = acc[t][v] * inv;
+        for (int v = 0; v < 4; ++v) {
+            const float lv = __shfl(lq, 4 * c + v);
+            const int qv = wq0 + qb * 16 + 4 * c + v;
+            if (qv < p.n_tok) {
+                float *orow = p.out + (((int64_t) b * p.n_tok + qv) * p.n_heads + h) * D;
+                const float inv = lv > 0.0f ? 1.0f / lv : 0.0f;
+#pragma unroll
+                for (int t = 0; t < NT; ++t) orow[col_elem(t * 16 + n)] = acc[qb][t][v] * inv;
+            }
         }
     }
 }
@@ -336,13 +455,13 @@ bool launch_prefill(const PrefillParams &p, hipStream_t stream) {
     const int64_t stage_threads = (int64_t) p.n_batch * p.n_tok * p.n_kv * nblk * 2;
     hipLaunchKernelGGL(stage_kernel, dim3((unsigned) ((stage_threads + 255) / 256)), dim3(256), 0,
                        stream, p);
-    constexpr int QW = 4;
-    const int n_qt = (p.n_tok + 16 * QW - 1) / (16 * QW);
+    constexpr int QW = 4, QB = 2;  // 4 waves x 32 queries
+    const int n_qt = (p.n_tok + 16 * QB * QW - 1) / (16 * QB * QW);
     const dim3 grid((unsigned) ((int64_t) p.n_batch * p.n_heads * n_qt));
     if (p.g.head_dim == 128)
-        hipLaunchKernelGGL((prefill_kernel<128, QW>), grid, dim3(64 * QW), 0, stream, p);
+        hipLaunchKernelGGL((prefill_kernel<128, QW, QB>), grid, dim3(64 * QW), 0, stream, p);
     else if (p.g.head_dim == 64)
-        hipLaunchKernelGGL((prefill_kernel<64, QW>), grid, dim3(64 * QW), 0, stream, p);
+        hipLaunchKernelGGL((prefill_kernel<64, QW, QB>), grid, dim3(64 * QW), 0, stream, p);
     else
         return false;
     const int64_t commit_threads = (int64_t) p.n_batch * p.n_tok * p.n_kv * nblk;
