@@ -408,7 +408,7 @@ def main():
     achieved = launch_bytes / (launch_ms * 1e-3) / 1e9
     log(f"[bench] {ms_per_step:.3f} ms/step, {value:.1f} GB/s; per launch "
         f"{launch_ms * 1e3:.2f} us -> {achieved:.1f} GB/s")
-    kernel = "decode_kernel<128, 1, 1, %s>" % ("true" if fused else "false")
+    kernel = "decode_kernel<128, 1, 2, %s>" % ("true" if fused else "false")
     traffic = read_traffic(args.config)
 
     result = {

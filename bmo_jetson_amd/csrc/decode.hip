@@ -39,13 +39,16 @@
 //
 // V side: masking a code dword with 0x000F000F (0x00F000F0) leaves two fp16
 // subnormals equal to c * 2^-24 (c * 2^-20); v_fma_mix_f32 reads them next to
-// the fp32 weight p * d pre-scaled by 2^24 (2^20) and accumulates
-// sum_i p_i d_i c_ie in fp32; 8 sum_i p_i d_i is subtracted at the end.
+// the fp32 weight 2^24 * p * d and accumulates sum_i p_i d_i c_ie in fp32
+// (16 times that for the high nibbles, rescaled at the end); 8 sum_i p_i d_i
+// is subtracted at the end.
 //
 // Softmax is online per lane (running max m, sum l, acc[32]).  A lane
 // rescales only when a score exceeds its running max by more than 8 (log2
 // units), so weights stay below 2^8 and rescaling is rare after the first
-// keys; the result does not depend on the threshold.  At the end every lane
+// keys; the result does not depend on the threshold.  Weights are carried
+// times 2^24 (the stored max is m - 24), which is the scale the subnormal
+// V codes need, so one multiply by the V scale makes a key's weight.  At the end every lane
 // is brought to the wave max, lanes sharing a block are summed by DPP
 // rotations, rows go through LDS and the workgroup's threads merge waves.
 //
@@ -73,6 +76,12 @@ constexpr float kTwo20 = 1048576.0f;
 constexpr int kQMax = 30583;      // 7 * (1 + 16 + 256 + 4096): largest |Q|
 constexpr int kQBias = 34952;     // 8 * (1 + 16 + 256 + 4096)
 constexpr float kRescale = 8.0f;  // lazy rescale threshold, log2 units
+// Weights are kept scaled by 2^24 (the running max is stored minus 24), so
+// the fp16-subnormal codes c * 2^-24 multiply them without a per-key scaling.
+constexpr float kWScale = 24.0f;
+// Running-max floor: finite, so a masked score (-inf) gives exp2(-inf - m) = 0
+// with no select.
+constexpr float kMaxFloor = -1.0e30f;
 
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
@@ -97,15 +106,30 @@ __device__ __forceinline__ float row_block_sum(float v) {
     return v;
 }
 
+// Wave-wide max / sum without LDS: DPP within each 16-lane row, then the
+// four row results through readlane.
+__device__ __forceinline__ float row_max(float v) {
+    v = fmaxf(v, dpp<0xB1>(v));   // lane ^ 1
+    v = fmaxf(v, dpp<0x4E>(v));   // lane ^ 2
+    v = fmaxf(v, dpp<0x124>(v));  // row_ror:4
+    return fmaxf(v, dpp<0x128>(v));  // row_ror:8
+}
+__device__ __forceinline__ float row_sum(float v) {
+    v += dpp<0xB1>(v);
+    v += dpp<0x4E>(v);
+    v += dpp<0x124>(v);
+    return v + dpp<0x128>(v);
+}
+__device__ __forceinline__ float lane_value(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
+    v = row_max(v);
+    return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
 }
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
-    return v;
+    v = row_sum(v);
+    return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
 }
 
 // K-side scorer: sum_e (c_e - 8) q_e of one block, before the block scale.
@@ -163,28 +187,36 @@ __device__ __forceinline__ void prep_digits(const float *__restrict__ qrow, floa
     }
 }
 
-// acc[e] += pd * c_e for the 32 elements of one block (acc in element order;
-// w4 holds plain codes 0..15).
-__device__ __forceinline__ void block_axpy(const uint4 &w4, float pd, float (&acc)[32]) {
-    const uint32_t w[4] = {w4.x, w4.y, w4.z, w4.w};
-    const float pl = pd * kTwo24;
-    const float ph = pd * kTwo20;
+// acc[e] += w * c_e * 2^-24 for elements 0..15 and w * c_e * 2^-20 for
+// elements 16..31 of one block (acc in element order; w4 holds plain codes
+// 0..15): a masked code dword is a pair of fp16 subnormals c * 2^-24 (low
+// nibble of a byte) or c * 2^-20 (high nibble), which v_fma_mix_f32 reads
+// directly.  The caller scales elements 16..31 by 1/16 at the end.
+__device__ __forceinline__ void block_axpy(const uint4 &w4, float w, float (&acc)[32]) {
+    const uint32_t wd[4] = {w4.x, w4.y, w4.z, w4.w};
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-        const uint32_t w8 = w[c] >> 8;
-        const half2_t A = __builtin_bit_cast(half2_t, w[c] & 0x000F000Fu);
-        const half2_t B = __builtin_bit_cast(half2_t, w[c] & 0x00F000F0u);
+        const uint32_t w8 = wd[c] >> 8;
+        const half2_t A = __builtin_bit_cast(half2_t, wd[c] & 0x000F000Fu);
+        const half2_t B = __builtin_bit_cast(half2_t, wd[c] & 0x00F000F0u);
         const half2_t C = __builtin_bit_cast(half2_t, w8 & 0x000F000Fu);
         const half2_t E = __builtin_bit_cast(half2_t, w8 & 0x00F000F0u);
-        acc[4 * c + 0] = __builtin_fmaf((float) A.x, pl, acc[4 * c + 0]);
-        acc[4 * c + 2] = __builtin_fmaf((float) A.y, pl, acc[4 * c + 2]);
-        acc[4 * c + 16] = __builtin_fmaf((float) B.x, ph, acc[4 * c + 16]);
-        acc[4 * c + 18] = __builtin_fmaf((float) B.y, ph, acc[4 * c + 18]);
-        acc[4 * c + 1] = __builtin_fmaf((float) C.x, pl, acc[4 * c + 1]);
-        acc[4 * c + 3] = __builtin_fmaf((float) C.y, pl, acc[4 * c + 3]);
-        acc[4 * c + 17] = __builtin_fmaf((float) E.x, ph, acc[4 * c + 17]);
-        acc[4 * c + 19] = __builtin_fmaf((float) E.y, ph, acc[4 * c + 19]);
+        acc[4 * c + 0] = __builtin_fmaf((float) A.x, w, acc[4 * c + 0]);
+        acc[4 * c + 2] = __builtin_fmaf((float) A.y, w, acc[4 * c + 2]);
+        acc[4 * c + 16] = __builtin_fmaf((float) B.x, w, acc[4 * c + 16]);
+        acc[4 * c + 18] = __builtin_fmaf((float) B.y, w, acc[4 * c + 18]);
+        acc[4 * c + 1] = __builtin_fmaf((float) C.x, w, acc[4 * c + 1]);
+        acc[4 * c + 3] = __builtin_fmaf((float) C.y, w, acc[4 * c + 3]);
+        acc[4 * c + 17] = __builtin_fmaf((float) E.x, w, acc[4 * c + 17]);
+        acc[4 * c + 19] = __builtin_fmaf((float) E.y, w, acc[4 * c + 19]);
     }
+}
+
+// fp32 value of the fp16 in the low (HI = false) or high half of a dword.
+template <bool HI>
+__device__ __forceinline__ float half_of(uint32_t v) {
+    const half2_t h = __builtin_bit_cast(half2_t, v);
+    return HI ? (float) h.y : (float) h.x;
 }
 
 }  // namespace
@@ -266,9 +298,14 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     }
     score.sq = s_sq[wave][blk];
 
-    float m = -INFINITY;  // running max of this lane's keys (log2 domain)
-    float l = 0.0f;       // running sum of this lane's keys (each key counted LPK times)
-    float csum = 0.0f;    // sum of p*d over this lane's keys
+    // Softmax state of this lane's keys (log2 domain): mm = running max - 24,
+    // mt = running max + 8 (the lazy rescale threshold), l = sum of weights
+    // times 2^24 (each key counted LPK times), csum = sum of weight * V scale
+    // times 2^24.
+    float mm = kMaxFloor;
+    float mt = kMaxFloor;
+    float l = 0.0f;
+    float csum = 0.0f;
     float acc[32];
 #pragma unroll
     for (int e = 0; e < 32; ++e) acc[e] = 0.0f;
@@ -303,11 +340,12 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
             }
             s_new = key_sum<LPK>(s_new);
             if (kk == 0) {
-                const float vd_new = f16_bits_to_f32(vd16);
-                m = s_new;
-                l = 1.0f;  // exp2(s_new - m)
-                csum = vd_new;
-                block_axpy(make_uint4(vq[0], vq[1], vq[2], vq[3]), vd_new, acc);
+                const float w_new = 16777216.0f * f16_bits_to_f32(vd16);  // 2^24 * exp2(0) * d
+                mm = s_new - kWScale;
+                mt = s_new + kRescale;
+                l = 16777216.0f;
+                csum = w_new;
+                block_axpy(make_uint4(vq[0], vq[1], vq[2], vq[3]), w_new, acc);
             }
         }
     }
@@ -316,22 +354,24 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
         const int slot = (g0 + it) * G + kk;
         bool ok = slot < window;
         if constexpr (FUSED) ok = ok && slot != cur;
-        const float sk = key_sum<LPK>(f16_bits_to_f32(T.sc & 0xFFFFu) * score(T.k));
+        const float sk = key_sum<LPK>(score(T.k) * half_of<false>(T.sc));
         const float s = ok ? sk : -INFINITY;
-        const bool need = s > m + kRescale;
+        const bool need = s > mt;
         if (__any(need)) {
-            const float alpha = need ? ((m == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m - s)) : 1.0f;
-            m = need ? s : m;
+            const float mm_new = need ? s - kWScale : mm;
+            const float alpha = __builtin_amdgcn_exp2f(mm - mm_new);
+            mm = mm_new;
+            mt = need ? s + kRescale : mt;
             l *= alpha;
             csum *= alpha;
 #pragma unroll
             for (int e = 0; e < 32; ++e) acc[e] *= alpha;
         }
-        const float pk = ok ? __builtin_amdgcn_exp2f(s - m) : 0.0f;
+        const float pk = __builtin_amdgcn_exp2f(s - mm);  // 2^24 * weight; 0 if masked
         l += pk;
-        const float pd = pk * f16_bits_to_f32(T.sc >> 16);
-        csum += pd;
-        block_axpy(T.v, pd, acc);
+        const float w = pk * half_of<true>(T.sc);
+        csum += w;
+        block_axpy(T.v, w, acc);
     };
     // Steady state: every load is unconditional, so the wait before a group's
     // compute is for that group's loads only (a conditional prefetch would
@@ -355,19 +395,23 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
         }
     }
 
-    // Bring every lane to the wave max, fold the -8 code offset, sum the lanes
-    // of each row that share a block, and publish the row sums.
-    const float m_wave = wave_max(m);
+    // Bring every lane to the wave max, undo the 2^-20 scale of elements
+    // 16..31, fold the -8 code offset, and sum the lanes of each row that
+    // share a block.
+    const float m_wave = wave_max(mm);
     {
-        const float f = (m == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m - m_wave);
+        const float f = __builtin_amdgcn_exp2f(mm - m_wave);
         l *= f;
         csum *= f;
 #pragma unroll
         for (int e = 0; e < 32; ++e) acc[e] *= f;
     }
     const float l_wave = wave_sum(l) * (1.0f / LPK);
+    const float c8 = -8.0f / 16777216.0f * csum;  // -8 * sum of p * d, in acc units
 #pragma unroll
-    for (int e = 0; e < 32; ++e) acc[e] = row_block_sum<LPK>(__builtin_fmaf(-8.0f, csum, acc[e]));
+    for (int e = 0; e < 32; ++e)
+        acc[e] = row_block_sum<LPK>(e < 16 ? acc[e] + c8 : __builtin_fmaf(acc[e], 0.0625f, c8));
+    // l_wave is 2^24 times the weight sum: the output divides by it times 2^-24
     const int row = lane >> 4;
     if ((lane & 15) < LPK) {
         float4 *dst = reinterpret_cast<float4 *>(s_acc + (wave * ROWS + row) * D + blk * kQK);
@@ -389,7 +433,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     float L = 0.0f;  // sum of weights of the whole window
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
-        fw[w] = (s_m[w] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(s_m[w] - M);
+        fw[w] = __builtin_amdgcn_exp2f(s_m[w] - M);
         L = __builtin_fmaf(fw[w], s_l[w], L);
     }
     // Thread t sums the rows of waves w = t / D (mod the number of row
@@ -416,7 +460,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
         }
         part[j] = a;
     }
-    const float inv_l = (L > 0.0f) ? 1.0f / L : 0.0f;
+    const float inv_l = (L > 0.0f) ? 16777216.0f / L : 0.0f;  // L is 2^24 times the weight sum
     if constexpr (NPART == 1) {
 #pragma unroll
         for (int j = 0; j < PER_T; ++j) out_row[threadIdx.x + j * TPB] = part[0 + j] * inv_l;
@@ -448,12 +492,13 @@ struct Shape {
     int nw, pf;
 };
 
-// Workgroup shape per call: one wave per (entry, head) unit when there are
-// enough units to fill the chip, else enough waves per unit for about 512
-// waves in all.  BMO_ATTN_SHAPE = "nw,pf" overrides the choice (tuning;
+// Workgroup shape per call: one wave per (entry, head) unit with two groups
+// of loads in flight when there are enough units to fill the chip (measured
+// best over sustained runs of BASELINE config 3), else enough waves per unit
+// for about 512 waves in all.  BMO_ATTN_SHAPE = "nw,pf" overrides the choice (tuning;
 // unknown shapes fall back to the default).
 Shape pick_shape(int64_t units, int n_groups) {
-    Shape s{1, 1};
+    Shape s{1, 2};
     if (units < 128) s = Shape{8, 1};
     else if (units < 256) s = Shape{4, 1};
     else if (units < 512) s = Shape{2, 1};
@@ -474,6 +519,7 @@ bool launch_shape(const DecodeParams &p, bool fused, hipStream_t stream, const S
     }
     BMO_SHAPE(1, 1)
     BMO_SHAPE(1, 2)
+    BMO_SHAPE(1, 3)
     BMO_SHAPE(2, 1)
     BMO_SHAPE(4, 1)
     BMO_SHAPE(8, 1)

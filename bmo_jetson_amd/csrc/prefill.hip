@@ -35,6 +35,7 @@
 // and the weights P in fp16, accumulation in fp32.  K and V values fit fp16
 // as the reference's F16 cache requires.
 #include <math.h>
+#include <stdlib.h>
 
 #include "kernels.hpp"
 #include "q4_0_device.hpp"
@@ -50,6 +51,9 @@ typedef float float4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kTK = 32;          // keys per tile
 constexpr float kRescale = 8.0f; // lazy rescale threshold, log2 units
+// Running-max floor: finite, so a masked score (-inf) gives exp2(-inf - m)
+// = 0 with no select, and far below any real score.
+constexpr float kMaxFloor = -1.0e30f;
 
 __device__ __forceinline__ float bf16_to_f32(uint32_t bits) {
     return __builtin_bit_cast(float, bits << 16);
@@ -169,10 +173,10 @@ __global__ __launch_bounds__(256) void commit_kernel(PrefillParams p) {
         *reinterpret_cast<const uint32_t *>(src + p.sg.scale_offset(i, blk));
 }
 
-// Two workgroups per CU: the register budget that keeps the accumulators in
-// architectural registers without spilling.
+// Eight waves per CU (two waves per SIMD): the register budget that keeps
+// the accumulators in architectural registers without spilling.
 template <int D, int QW, int QB>
-__global__ __launch_bounds__(64 * QW, 2) void prefill_kernel(PrefillParams p) {
+__global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams p) {
     constexpr int NBLK = D / kQK;
     // LDS rows (fp16): K rows padded to 68 dwords so that the 16 lanes of an
     // operand read (16 keys, one 16-byte chunk each) hit 16 distinct 4-bank
@@ -329,7 +333,7 @@ __global__ __launch_bounds__(64 * QW, 2) void prefill_kernel(PrefillParams p) {
     float4_t acc[QB][NT];
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
-        m[qb] = -INFINITY;
+        m[qb] = kMaxFloor;
         l[qb] = 0.0f;
 #pragma unroll
         for (int t = 0; t < NT; ++t) acc[qb][t] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
@@ -375,8 +379,7 @@ __global__ __launch_bounds__(64 * QW, 2) void prefill_kernel(PrefillParams p) {
             tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
             const bool need = tmax > m[qb] + kRescale;
             if (__any(need)) {
-                const float alpha =
-                    need ? ((m[qb] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m[qb] - tmax)) : 1.0f;
+                const float alpha = need ? __builtin_amdgcn_exp2f(m[qb] - tmax) : 1.0f;
                 m[qb] = need ? tmax : m[qb];
                 l[qb] *= alpha;
                 // acc rows are queries 4c + v: fetch their alphas from lanes 4c + v
@@ -391,8 +394,7 @@ __global__ __launch_bounds__(64 * QW, 2) void prefill_kernel(PrefillParams p) {
             for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
-                    const float pv =
-                        (s[qb][sub][v] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(s[qb][sub][v] - m[qb]);
+                    const float pv = __builtin_amdgcn_exp2f(s[qb][sub][v] - m[qb]);
                     l[qb] += pv;
                     pop[qb][sub * 4 + v] = (_Float16) pv;
                 }
@@ -455,15 +457,25 @@ bool launch_prefill(const PrefillParams &p, hipStream_t stream) {
     const int64_t stage_threads = (int64_t) p.n_batch * p.n_tok * p.n_kv * nblk * 2;
     hipLaunchKernelGGL(stage_kernel, dim3((unsigned) ((stage_threads + 255) / 256)), dim3(256), 0,
                        stream, p);
-    constexpr int QW = 4, QB = 2;  // 4 waves x 32 queries
-    const int n_qt = (p.n_tok + 16 * QB * QW - 1) / (16 * QB * QW);
-    const dim3 grid((unsigned) ((int64_t) p.n_batch * p.n_heads * n_qt));
-    if (p.g.head_dim == 128)
-        hipLaunchKernelGGL((prefill_kernel<128, QW, QB>), grid, dim3(64 * QW), 0, stream, p);
-    else if (p.g.head_dim == 64)
-        hipLaunchKernelGGL((prefill_kernel<64, QW, QB>), grid, dim3(64 * QW), 0, stream, p);
-    else
+    // 32 queries per wave; 8 waves (256 queries, one workgroup per chunk of
+    // a head) or 4.  BMO_PREFILL_WAVES = 4 | 8 overrides (tuning).
+    int qw = p.n_tok > 128 ? 8 : 4;
+    if (const char *e = std::getenv("BMO_PREFILL_WAVES")) qw = std::atoi(e) == 4 ? 4 : 8;
+    const int qt = 32 * qw;
+    const dim3 grid((unsigned) ((int64_t) p.n_batch * p.n_heads * ((p.n_tok + qt - 1) / qt)));
+    if (p.g.head_dim == 128) {
+        if (qw == 8)
+            hipLaunchKernelGGL((prefill_kernel<128, 8, 2>), grid, dim3(512), 0, stream, p);
+        else
+            hipLaunchKernelGGL((prefill_kernel<128, 4, 2>), grid, dim3(256), 0, stream, p);
+    } else if (p.g.head_dim == 64) {
+        if (qw == 8)
+            hipLaunchKernelGGL((prefill_kernel<64, 8, 2>), grid, dim3(512), 0, stream, p);
+        else
+            hipLaunchKernelGGL((prefill_kernel<64, 4, 2>), grid, dim3(256), 0, stream, p);
+    } else {
         return false;
+    }
     const int64_t commit_threads = (int64_t) p.n_batch * p.n_tok * p.n_kv * nblk;
     hipLaunchKernelGGL(commit_kernel, dim3((unsigned) ((commit_threads + 255) / 256)), dim3(256), 0,
                        stream, p);

@@ -321,7 +321,7 @@ def test_api_errors_on_device(gpu):
 
 # every (waves per unit, prefetch depth) shape compiled into launch_shape()
 # (decode.hip)
-SHAPES = ["1,1", "1,2", "2,1", "4,1", "8,1", "8,2", "16,1"]
+SHAPES = ["1,1", "1,2", "1,3", "2,1", "4,1", "8,1", "8,2", "16,1"]
 
 
 @pytest.mark.parametrize("shape", SHAPES)
