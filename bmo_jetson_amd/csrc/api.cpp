@@ -105,38 +105,49 @@ float f16_to_f32_host(uint16_t h) {
     return f;
 }
 
-// Copies the groups holding slots [t0, t0+n) of one stripe to host; *first
-// receives the first group's index.
+// Copies the groups holding slots [t0, t0+n) of one stripe to host, packed
+// back to back; *first receives the first group's index.
 hipError_t fetch_groups(const bmo_kv_ring_t *r, const uint8_t *stripe, int t0, int n,
                         std::vector<uint8_t> &buf, int *first) {
     const int G = bmo::keys_per_group(r->g.head_dim);
     const int g0 = t0 / G, g1 = (t0 + n - 1) / G;
     *first = g0;
     buf.resize((size_t) (g1 - g0 + 1) * bmo::kGroupBytes);
-    return hipMemcpy(buf.data(), stripe + (int64_t) g0 * bmo::kGroupBytes, buf.size(),
-                     hipMemcpyDeviceToHost);
+    return hipMemcpy2D(buf.data(), bmo::kGroupBytes, stripe + (int64_t) g0 * r->g.group_stride,
+                       (size_t) r->g.group_stride, bmo::kGroupBytes, (size_t) (g1 - g0 + 1),
+                       hipMemcpyDeviceToHost);
+}
+
+// Writes packed groups back to their places in a stripe.
+hipError_t store_groups(const bmo_kv_ring_t *r, uint8_t *stripe, const std::vector<uint8_t> &buf,
+                        int first) {
+    return hipMemcpy2D(stripe + (int64_t) first * r->g.group_stride, (size_t) r->g.group_stride,
+                       buf.data(), bmo::kGroupBytes, bmo::kGroupBytes,
+                       buf.size() / bmo::kGroupBytes, hipMemcpyHostToDevice);
 }
 
 // ggml block (scale bits, 16 code bytes) of K (which 0) or V (which 1) at
-// slot, block blk, from a host copy of groups starting at group `first`.
+// slot, block blk, from packed groups starting at group `first`.
 void read_block(const bmo::RingGeom &g, const std::vector<uint8_t> &buf, int first, int which,
                 int slot, int blk, uint16_t *d, uint8_t *qs) {
+    const bmo::RingGeom pg = bmo::packed_stripe_geom(g);
     const int64_t base = (int64_t) first * bmo::kGroupBytes;
-    const uint8_t *codes = buf.data() + (which == 0 ? g.kcode_offset(slot, blk)
-                                                     : g.vcode_offset(slot, blk)) - base;
+    const uint8_t *codes = buf.data() + (which == 0 ? pg.kcode_offset(slot, blk)
+                                                     : pg.vcode_offset(slot, blk)) - base;
     const uint8_t flip = which == 0 ? bmo::kKCodeZero : 0;
     for (int j = 0; j < 16; ++j) qs[j] = codes[j] ^ flip;
-    std::memcpy(d, buf.data() + g.scale_offset(slot, blk) - base + 2 * which, 2);
+    std::memcpy(d, buf.data() + pg.scale_offset(slot, blk) - base + 2 * which, 2);
 }
 
 void write_block(const bmo::RingGeom &g, std::vector<uint8_t> &buf, int first, int which,
                  int slot, int blk, uint16_t d, const uint8_t *qs) {
+    const bmo::RingGeom pg = bmo::packed_stripe_geom(g);
     const int64_t base = (int64_t) first * bmo::kGroupBytes;
-    uint8_t *codes = buf.data() + (which == 0 ? g.kcode_offset(slot, blk)
-                                               : g.vcode_offset(slot, blk)) - base;
+    uint8_t *codes = buf.data() + (which == 0 ? pg.kcode_offset(slot, blk)
+                                               : pg.vcode_offset(slot, blk)) - base;
     const uint8_t flip = which == 0 ? bmo::kKCodeZero : 0;
     for (int j = 0; j < 16; ++j) codes[j] = qs[j] ^ flip;
-    std::memcpy(buf.data() + g.scale_offset(slot, blk) - base + 2 * which, &d, 2);
+    std::memcpy(buf.data() + pg.scale_offset(slot, blk) - base + 2 * which, &d, 2);
 }
 
 }  // namespace
@@ -249,11 +260,11 @@ int bmo_kv_ring_reset(bmo_kv_ring_t *r, int session, void *stream) {
         if (session == -1) {
             bmo::launch_clear(r->mem, g.total_bytes(), 0, 1, (hipStream_t) stream);
         } else {
-            // session s of layer l: n_kv_heads contiguous stripes
+            // group g of layer l holds the session's n_kv_heads groups side by
+            // side; (layer, group) pairs are group_stride apart
             bmo::launch_clear(r->mem + g.stripe_offset(0, session, 0),
-                              (int64_t) g.n_kv_heads * g.stripe_bytes,
-                              (int64_t) g.n_sessions * g.n_kv_heads * g.stripe_bytes, g.n_layers,
-                              (hipStream_t) stream);
+                              (int64_t) g.n_kv_heads * bmo::kGroupBytes, g.group_stride,
+                              g.n_layers * g.n_groups, (hipStream_t) stream);
         }
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return hip_fail(r, e, "bmo_kv_ring_reset");
@@ -549,9 +560,7 @@ int64_t bmo_kv_ring_import_q4_0(bmo_kv_ring_t *r, int layer, int session, int wh
                     std::memcpy(&d16, blkp, 2);
                     write_block(g, buf, first, which, t_start + ti, b, d16, blkp + 2);
                 }
-            if (hipMemcpy(stripe + (int64_t) first * bmo::kGroupBytes, buf.data(), buf.size(),
-                          hipMemcpyHostToDevice) != hipSuccess)
-                return BMO_ATTN_READ_ERR_NULL;
+            if (store_groups(r, stripe, buf, first) != hipSuccess) return BMO_ATTN_READ_ERR_NULL;
         }
         return need;
     } catch (...) {

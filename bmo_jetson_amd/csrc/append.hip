@@ -53,18 +53,20 @@ __global__ __launch_bounds__(256) void append_kernel(AppendParams p) {
 }
 
 // Zero state of the ring (ring_layout.hpp): K code bytes 0x88, the rest 0.
-// blockIdx.y selects the range; ranges are whole groups.
+// Ranges are whole groups; blockIdx.y strides over the ranges.
 __global__ __launch_bounds__(256) void clear_kernel(uint8_t *base, int64_t range_bytes,
-                                                    int64_t range_stride) {
-    uint4 *dst = reinterpret_cast<uint4 *>(base + (int64_t) blockIdx.y * range_stride);
+                                                    int64_t range_stride, int n_ranges) {
     const int64_t n = range_bytes / 16;
     constexpr int per_group = kGroupBytes / 16;
     constexpr int k_codes = kVCodeOff / 16;
     const uint32_t kz = 0x01010101u * kKCodeZero;
-    for (int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; i < n;
-         i += (int64_t) gridDim.x * blockDim.x) {
-        const uint32_t w = (int) (i % per_group) < k_codes ? kz : 0u;
-        dst[i] = make_uint4(w, w, w, w);
+    for (int r = blockIdx.y; r < n_ranges; r += gridDim.y) {
+        uint4 *dst = reinterpret_cast<uint4 *>(base + (int64_t) r * range_stride);
+        for (int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; i < n;
+             i += (int64_t) gridDim.x * blockDim.x) {
+            const uint32_t w = (int) (i % per_group) < k_codes ? kz : 0u;
+            dst[i] = make_uint4(w, w, w, w);
+        }
     }
 }
 
@@ -73,8 +75,9 @@ void launch_clear(uint8_t *base, int64_t range_bytes, int64_t range_stride, int 
     if (range_bytes <= 0 || n_ranges <= 0) return;
     const int64_t vecs = range_bytes / 16;
     const unsigned gx = (unsigned) std::min<int64_t>((vecs + 255) / 256, 8192);
-    hipLaunchKernelGGL(clear_kernel, dim3(gx, (unsigned) n_ranges), dim3(256), 0, stream, base,
-                       range_bytes, range_stride);
+    const unsigned gy = (unsigned) std::min(n_ranges, 65535);
+    hipLaunchKernelGGL(clear_kernel, dim3(gx, gy), dim3(256), 0, stream, base, range_bytes,
+                       range_stride, n_ranges);
 }
 
 void launch_append(const AppendParams &p, hipStream_t stream) {

@@ -268,7 +268,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     };
     typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
     auto load = [&](int it, Grp &T) {
-        const uint8_t *gp = stripe + (int64_t) (g0 + it) * kGroupBytes;
+        const uint8_t *gp = stripe + (int64_t) (g0 + it) * g.group_stride;
         const u32x4 kc = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(gp + lane * 16));
         const u32x4 vc =
             __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(gp + kVCodeOff + lane * 16));

@@ -224,14 +224,14 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams 
     const int slot0 = pos0 % n_ctx;  // ring slot of position pos0
     const uint8_t *ring = p.base + p.g.stripe_offset(p.layer, sid, kvh);
     const uint8_t *stage = p.stage + p.sg.stripe_offset(0, b, kvh);
-    // Byte offsets inside a stripe (ring_layout.hpp) with the group size
-    // known at compile time.
+    // Byte offsets from a stripe's group 0 (ring_layout.hpp), the group size
+    // known at compile time; gs is the stripe's group stride.
     constexpr int G = keys_per_group(D);
-    auto code_off = [](int slot, int bb, int which) {
-        return (slot / G) * kGroupBytes + (slot % G) * (D / 2) + bb * 16 + which * kVCodeOff;
+    auto code_off = [](int slot, int bb, int which, int64_t gs) {
+        return (slot / G) * gs + (slot % G) * (D / 2) + bb * 16 + which * kVCodeOff;
     };
-    auto scale_off = [](int slot, int bb) {
-        return (slot / G) * kGroupBytes + kScaleOff + ((slot % G) * NBLK + bb) * 4;
+    auto scale_off = [](int slot, int bb, int64_t gs) {
+        return (slot / G) * gs + kScaleOff + ((slot % G) * NBLK + bb) * 4;
     };
 
     // Raw tile bytes, fetched PF tiles ahead: this thread's items.  Every
@@ -261,8 +261,9 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams 
             rslot += rslot < 0 ? n_ctx : 0;
             const int slot = !live ? 0 : old ? rslot : t - pos0;
             const uint8_t *src = old ? ring : stage;
-            rw[j] = *reinterpret_cast<const uint2 *>(src + code_off(slot, bb, which) + 8 * hf);
-            rd[j] = *reinterpret_cast<const uint16_t *>(src + scale_off(slot, bb) + 2 * which);
+            const int64_t gs = old ? p.g.group_stride : p.sg.group_stride;
+            rw[j] = *reinterpret_cast<const uint2 *>(src + code_off(slot, bb, which, gs) + 8 * hf);
+            rd[j] = *reinterpret_cast<const uint16_t *>(src + scale_off(slot, bb, gs) + 2 * which);
             rl[j] = live;
         }
     };

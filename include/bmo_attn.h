@@ -29,15 +29,14 @@
  *     Appends quantize bit-exactly as ggml quantize_row_q4_0_ref.
  *
  * Ring layout in HBM (what the kernels read; export/import convert to and
- * from ggml's 18-byte AoS blocks): one allocation of
- *   [n_layers][n_sessions][n_kv_heads] stripes of
- * bmo_kv_ring_stripe_bytes(head_dim, n_ctx) bytes.  A stripe holds the
- * n_ctx slots of one kv head in groups of G = 2048/head_dim slots; a group
- * is 2304 bytes: K codes [G][head_dim/2] (stored as code ^ 8 per nibble),
- * V codes [G][head_dim/2], then one dword per (slot, block) holding the K
- * scale (fp16, low half) and the V scale (high half).  Slot of absolute
- * position p is p % n_ctx.  A fresh or reset slot holds the ggml block with
- * d = 0 and all codes 0.
+ * from ggml's 18-byte AoS blocks): the n_ctx slots of one (layer, session,
+ * kv head) -- a stripe -- are cut into groups of G = 2048/head_dim slots; a
+ * group is 2304 bytes: K codes [G][head_dim/2] (stored as code ^ 8 per
+ * nibble), V codes [G][head_dim/2], then one dword per (slot, block) holding
+ * the K scale (fp16, low half) and the V scale (high half).  One allocation
+ * holds the groups as [n_layers][groups per stripe][n_sessions][n_kv_heads].
+ * Slot of absolute position p is p % n_ctx.  A fresh or reset slot holds the
+ * ggml block with d = 0 and all codes 0.
  */
 #ifndef BMO_ATTN_H
 #define BMO_ATTN_H
@@ -72,8 +71,8 @@ typedef struct bmo_kv_ring bmo_kv_ring_t;
 
 /* ---- allocation (replaces bmo_init_kv_cache, src/bmo.cpp:1348-1508) ------- */
 
-/* Bytes of one (layer, session, kv head) stripe (its K and V); 0 for an
- * unsupported head_dim or n_ctx <= 0. */
+/* Bytes of one (layer, session, kv head) stripe (its K and V, in groups that
+ * are not contiguous); 0 for an unsupported head_dim or n_ctx <= 0. */
 BMO_ATTN_API int64_t bmo_kv_ring_stripe_bytes(int head_dim, int n_ctx);
 
 /* Allocates and zeroes a ring on the current HIP device.  head_dim must be 64
