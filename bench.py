@@ -341,6 +341,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-b1", action="store_true")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only run the cfg5 chunked-prefill leg and print its JSON (profiling)")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="only run a plain device copy of this size (rocprof PMC calibration)")
     args = ap.parse_args()
@@ -365,6 +367,10 @@ def main():
             b.copy_(a)
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_read": n * 4, "copy_bytes_written": n * 4}))
+        return
+
+    if args.prefill_only:
+        print(json.dumps({"prefill": bench_prefill(torch)}), flush=True)
         return
 
     from bmo_jetson_amd import KVRing
