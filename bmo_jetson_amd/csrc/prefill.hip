@@ -34,6 +34,7 @@
 // Operands: q (bf16 inputs, scaled by scale*log2 e) and the dequantized K, V
 // and the weights P in fp16, accumulation in fp32.  K and V values fit fp16
 // as the reference's F16 cache requires.
+#include <limits.h>
 #include <math.h>
 #include <stdlib.h>
 
@@ -67,6 +68,11 @@ __device__ __forceinline__ half4_t lds_read_tr16(const _Float16 *p) {
     typedef __attribute__((address_space(3))) fp16x4 lds_fp16x4;
     return __builtin_bit_cast(half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_fp16x4 *) p));
 }
+
+// Maximum without operand canonicalization (v_maximum3_f32): scores are
+// never NaN, and fmaxf's quieting of signalling NaNs costs an instruction per
+// operand.
+__device__ __forceinline__ float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 
 // Workgroup barrier for LDS hand-off only: waits for this wave's LDS
 // operations, not for its global loads (__syncthreads' fence would also wait
@@ -187,15 +193,28 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams 
     constexpr int QWV = 16 * QB;   // queries per wave
     constexpr int QT = QWV * QW;   // queries per workgroup
     constexpr int NT = D / 16;     // output column tiles
+    constexpr int NTHR = 64 * QW;
     // dequantization items per tile: (K/V, key, block, 8-byte half)
     constexpr int ITEMS = 2 * kTK * NBLK * 2;
-    constexpr int IPT = (ITEMS + 64 * QW - 1) / (64 * QW);
+    constexpr int IPT = (ITEMS + NTHR - 1) / NTHR;
+    constexpr int G = keys_per_group(D);
+    static_assert((G & (G - 1)) == 0, "slot groups are a power of two");
+
+    // Per-wave staging (wave-private): the wave's query rows (bf16) at the
+    // start, its output rows (fp32, one query block at a time) at the end, so
+    // that both move between HBM and LDS as whole 16-byte row pieces.
+    constexpr int QROW = D + 8;    // bf16 per staged query row
+    constexpr int OROW = D + 4;    // fp32 per staged output row
+    constexpr int WSTAGE = (QWV * QROW * 2 > 16 * OROW * 4 ? QWV * QROW * 2 : 16 * OROW * 4) / 16;
 
     __shared__ __align__(16) _Float16 sK[2][kTK * KROW];
     __shared__ __align__(16) _Float16 sV[2][kTK * VROW];
+    __shared__ __align__(16) uint4 sW[QW][WSTAGE];
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    // wave-uniform (readfirstlane), so that everything derived from it --
+    // the tile skip, the whole-tile test -- is a scalar branch
+    const int wave = __builtin_amdgcn_readfirstlane((int) threadIdx.x >> 6);
     const int n_qt = (p.n_tok + QT - 1) / QT;
     const int qt = blockIdx.x % n_qt;
     const int unit = blockIdx.x / n_qt;
@@ -208,63 +227,75 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams 
     const int sid = p.session_ids ? p.session_ids[b] : b;
     const int pos0 = p.pos0[b];
     const int nq = min(QT, p.n_tok - i0);  // valid queries of this workgroup
-    if (sid < 0 || sid >= p.g.n_sessions || pos0 < 0) {
+    if (sid < 0 || sid >= p.g.n_sessions || pos0 < 0 || pos0 > INT_MAX - p.n_tok) {
         for (int e = threadIdx.x; e < nq * D; e += blockDim.x) {
             const int qi = e / D;
             p.out[(((int64_t) b * p.n_tok + i0 + qi) * p.n_heads + h) * D + e % D] = 0.0f;
         }
         return;
     }
-    // Positions are int: the API bounds them by pos0 + n_tok < 2^31.
     const int n_ctx = p.g.n_ctx;
     const int p_first = pos0 + i0;
     const int p_last = pos0 + i0 + nq - 1;
     const int k_lo = max(0, p_first - n_ctx + 1);
     const int n_tiles = (p_last - k_lo) / kTK + 1;
-    const int slot0 = pos0 % n_ctx;  // ring slot of position pos0
     const uint8_t *ring = p.base + p.g.stripe_offset(p.layer, sid, kvh);
     const uint8_t *stage = p.stage + p.sg.stripe_offset(0, b, kvh);
-    // Byte offsets from a stripe's group 0 (ring_layout.hpp), the group size
-    // known at compile time; gs is the stripe's group stride.
-    constexpr int G = keys_per_group(D);
-    auto code_off = [](int slot, int bb, int which, int64_t gs) {
-        return (slot / G) * gs + (slot % G) * (D / 2) + bb * 16 + which * kVCodeOff;
-    };
-    auto scale_off = [](int slot, int bb, int64_t gs) {
-        return (slot / G) * gs + kScaleOff + ((slot % G) * NBLK + bb) * 4;
-    };
+    const uint32_t ring_gs = (uint32_t) p.g.group_stride;
+    const uint32_t stage_gs = (uint32_t) p.sg.group_stride;
+
+    // This thread's items: item j is (K/V, key, block, 8-byte half) =
+    // (which, key, bb, hf) of every tile.  The fetch walks the tiles in order
+    // and keeps, per item, the position t of its key in the tile being
+    // fetched and that position's ring slot t % n_ctx.
+    int it_key[IPT];
+    uint32_t it_code[IPT], it_scale[IPT];  // byte offsets inside a group
+    int ft[IPT], fslot[IPT];
+    const int slot_step = kTK % n_ctx;
+#pragma unroll
+    for (int j = 0; j < IPT; ++j) {
+        const int it = min((int) threadIdx.x + j * NTHR, ITEMS - 1);
+        const int hf = it & 1;
+        const int bb = (it >> 1) % NBLK;
+        const int key = (it >> 1) / NBLK % kTK;
+        const int which = it / (2 * kTK * NBLK);
+        it_key[j] = key;
+        it_code[j] = bb * 16 + which * kVCodeOff + 8 * hf;
+        it_scale[j] = kScaleOff + bb * 4;  // the (K, V) scale dword
+        ft[j] = k_lo + key;
+        fslot[j] = ft[j] % n_ctx;
+    }
 
     // Raw tile bytes, fetched PF tiles ahead: this thread's items.  Every
-    // fetch issues its loads (an item past the chunk reads the stripe's slot
-    // 0 and is dequantized with scale 0), so the number of loads in flight
-    // is the same on every path and the compiler's waits stay exact; the
-    // liveness flag is applied at dequantization, not at the load.
-    constexpr int PF = 3;
+    // fetch issues its loads (a key past the chunk reads a ring slot and is
+    // dequantized with scale 0), so the number of loads in flight is the same
+    // on every path and the compiler's waits stay exact; the liveness flag is
+    // applied at dequantization, not at the load.
+    constexpr int PF = 7;
     static_assert((PF + 1) % 2 == 0, "LDS buffer parity must follow the unrolled slot");
     uint2 raw[PF + 1][IPT];
     uint32_t rawd[PF + 1][IPT];
     bool rawl[PF + 1][IPT];
-    auto fetch = [&](int tile, uint2 (&rw)[IPT], uint32_t (&rd)[IPT], bool (&rl)[IPT]) {
-        const int t0 = k_lo + tile * kTK;
+    auto fetch = [&](uint2 (&rw)[IPT], uint32_t (&rd)[IPT], bool (&rl)[IPT]) {
 #pragma unroll
         for (int j = 0; j < IPT; ++j) {
-            const int it = min((int) threadIdx.x + j * 64 * QW, ITEMS - 1);
-            const int hf = it & 1;
-            const int bb = (it >> 1) % NBLK;
-            const int key = (it >> 1) / NBLK % kTK;
-            const int which = it / (2 * kTK * NBLK);
-            const int t = t0 + key;
-            const bool live = t <= p_last && (int) threadIdx.x + j * 64 * QW < ITEMS;
-            const bool old = t < pos0;
-            // old position t: slot (slot0 + t - pos0) mod n_ctx, t - pos0 in [-n_ctx, 0)
-            int rslot = slot0 + (t - pos0);
-            rslot += rslot < 0 ? n_ctx : 0;
-            const int slot = !live ? 0 : old ? rslot : t - pos0;
-            const uint8_t *src = old ? ring : stage;
-            const int64_t gs = old ? p.g.group_stride : p.sg.group_stride;
-            rw[j] = *reinterpret_cast<const uint2 *>(src + code_off(slot, bb, which, gs) + 8 * hf);
-            rd[j] = *reinterpret_cast<const uint16_t *>(src + scale_off(slot, bb, gs) + 2 * which);
-            rl[j] = live;
+            const int t = ft[j];
+            // chunk keys come from the staging stripe (slot t - pos0); older
+            // keys, and keys past the chunk (not live), from the ring
+            const bool chunk = t >= pos0 && t <= p_last;
+            const int slot = chunk ? t - pos0 : fslot[j];
+            const uint8_t *gp = (chunk ? stage : ring) +
+                                (uint64_t) (uint32_t) (slot / G) * (chunk ? stage_gs : ring_gs);
+            const uint32_t row = (uint32_t) (slot % G);
+            rw[j] = *reinterpret_cast<const uint2 *>(gp + row * (D / 2) + it_code[j]);
+            // the whole scale dword: a 16-bit load would be zero-extended
+            // into a copy that hipcc places at the loop's back edge, waiting
+            // for the load there
+            rd[j] = *reinterpret_cast<const uint32_t *>(gp + row * (NBLK * 4) + it_scale[j]);
+            rl[j] = t <= p_last && (int) threadIdx.x + j * NTHR < ITEMS;
+            ft[j] = t + kTK;
+            const int ns = fslot[j] + slot_step;
+            fslot[j] = ns >= n_ctx ? ns - n_ctx : ns;
         }
     };
     // Dequantizes fetched items into LDS buffer `buf`: K and V row-major,
@@ -274,14 +305,15 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams 
                        const bool (&rl)[IPT]) {
 #pragma unroll
         for (int j = 0; j < IPT; ++j) {
-            const int it = threadIdx.x + j * 64 * QW;
+            const int it = threadIdx.x + j * NTHR;
             if (it < ITEMS) {
                 const int hf = it & 1;
                 const int bb = (it >> 1) % NBLK;
-                const int key = (it >> 1) / NBLK % kTK;
+                const int key = it_key[j];
                 const int which = it / (2 * kTK * NBLK);
                 const uint32_t flip = which == 0 ? 0x88888888u : 0u;  // K codes are stored as code ^ 8
-                const uint32_t d16 = rl[j] ? rd[j] : 0u;                 // scale 0 past the chunk
+                const uint32_t dw = which == 0 ? rd[j] & 0xFFFFu : rd[j] >> 16;
+                const uint32_t d16 = rl[j] ? dw : 0u;  // scale 0 past the chunk
                 const half8_t v0 = dequant_dword(rw[j].x ^ flip, d16);
                 const half8_t v1 = dequant_dword(rw[j].y ^ flip, d16);
                 _Float16 *dst = which == 0 ? &sK[buf][key * KROW + bb * kQK + 16 * hf]
@@ -300,14 +332,28 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams 
     const int c = lane >> 4;
     const int wq0 = i0 + wave * QWV;  // first query of this wave
     half8_t qop[QB][NBLK];
-    bool q_ok[QB];
-    int pq[QB];  // this lane's query positions (S^T layout)
+    int mrel[QB];  // this lane's query position minus 4c (mask arithmetic)
+    uint16_t *sq = reinterpret_cast<uint16_t *>(sW[wave]);
+    {
+        // the wave's QWV query rows, 16 bytes per lane and load, into LDS
+        constexpr int CPR = D / 8;  // 16-byte pieces per row
+#pragma unroll
+        for (int k = 0; k < QWV * CPR / 64; ++k) {
+            const int e = k * 64 + lane;
+            const int row = e / CPR, col = e % CPR;
+            const int qi = min(wq0 + row, p.n_tok - 1);
+            const uint4 x = *reinterpret_cast<const uint4 *>(
+                p.q + (((int64_t) b * p.n_tok + qi) * p.n_heads + h) * D + col * 8);
+            *reinterpret_cast<uint4 *>(sq + row * QROW + col * 8) = x;
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // wave-private: no barrier needed
+    }
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
         const int qi = wq0 + qb * 16 + n;
-        q_ok[qb] = qi < p.n_tok;
-        pq[qb] = pos0 + qi;
-        const uint16_t *qrow = p.q + (((int64_t) b * p.n_tok + (q_ok[qb] ? qi : 0)) * p.n_heads + h) * D;
+        const bool q_ok = qi < p.n_tok;
+        mrel[qb] = pos0 + qi - 4 * c;
+        const uint16_t *qrow = sq + (qb * 16 + n) * QROW;
         uint2 lo[NBLK], hi[NBLK];
 #pragma unroll
         for (int bb = 0; bb < NBLK; ++bb) {
@@ -322,23 +368,30 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams 
                                    hi[bb].x & 0xFFFFu, hi[bb].y & 0xFFFFu, hi[bb].x >> 16, hi[bb].y >> 16};
 #pragma unroll
             for (int r = 0; r < 8; ++r)
-                qop[qb][bb][r] = (_Float16) (q_ok[qb] ? bf16_to_f32(e[r]) * p.qscale : 0.0f);
+                qop[qb][bb][r] = (_Float16) (q_ok ? bf16_to_f32(e[r]) * p.qscale : 0.0f);
         }
     }
-    // this wave's query positions and the keys they may see
+    // this wave's query positions and the keys they may see (wave-uniform)
     const int wq1 = min(wq0 + QWV - 1, p.n_tok - 1);
     const int w_hi = pos0 + wq1;
     const int w_lo = pos0 + wq0 - n_ctx + 1;
 
-    float m[QB], l[QB];  // running max and this lane's part of the weight sum, per query block
+    // Accumulators: acc[qb][t] = O columns 16t..16t+15, and accl[qb] = P
+    // times a ones operand, whose every column is the weight sum of a query
+    // row; both use the D layout (lane l: column l % 16, queries 4c + v), so
+    // the final division needs no cross-lane exchange.
+    float m[QB];
     float4_t acc[QB][NT];
+    float4_t accl[QB];
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
         m[qb] = kMaxFloor;
-        l[qb] = 0.0f;
+        accl[qb] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int t = 0; t < NT; ++t) acc[qb][t] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
     }
+    const half8_t ones = {(_Float16) 1.0f, (_Float16) 1.0f, (_Float16) 1.0f, (_Float16) 1.0f,
+                          (_Float16) 1.0f, (_Float16) 1.0f, (_Float16) 1.0f, (_Float16) 1.0f};
 
     auto compute = [&](int buf, int t0) {
         if (wq0 >= p.n_tok || t0 > w_hi || t0 + kTK - 1 < w_lo) return;  // nothing to see
@@ -358,35 +411,46 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams 
                     s[qb][sub] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop[qb][bb], s[qb][sub], 0, 0, 0);
             }
         }
-        // mask (causal + window) unless every key of the tile is visible to
-        // every query of the wave
-        const bool whole = wq1 == wq0 + QWV - 1 && t0 + kTK - 1 <= pos0 + wq0 && t0 > w_hi - n_ctx;
+        // Mask (causal + window) unless every key of the tile is visible to
+        // every query of the wave.  Query rows past the chunk are left
+        // unmasked: their scores are finite and their outputs never stored.
+        const bool whole = t0 + kTK - 1 <= pos0 + wq0 && t0 > w_hi - n_ctx;
+        if (!whole) {
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) {
+                // key t0 + 16 sub + 4c + v is visible to query position P iff
+                // P - n_ctx < t <= P, i.e. 16 sub + v in (rel - n_ctx, rel]
+                const int rel = mrel[qb] - t0;
+#pragma unroll
+                for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const int kk = sub * 16 + v;
+                        const bool ok = kk <= rel && kk > rel - n_ctx;
+                        s[qb][sub][v] = ok ? s[qb][sub][v] : -INFINITY;
+                    }
+            }
+        }
         half8_t pop[QB];
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
-            float tmax = -INFINITY;
-#pragma unroll
-            for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    if (!whole) {
-                        const int t = t0 + sub * 16 + 4 * c + v;
-                        const bool ok = q_ok[qb] && t <= pq[qb] && t > pq[qb] - n_ctx;
-                        s[qb][sub][v] = ok ? s[qb][sub][v] : -INFINITY;
-                    }
-                    tmax = fmaxf(tmax, s[qb][sub][v]);
-                }
-            tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-            tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-            const bool need = tmax > m[qb] + kRescale;
-            if (__any(need)) {
+            // This lane's 8 scores against the running max; the exact
+            // per-query maximum (a cross-lane reduction) is only needed when
+            // some score exceeds the running max by kRescale.
+            float tmax = vmax(vmax(vmax(s[qb][0][0], s[qb][0][1]), s[qb][0][2]),
+                              vmax(vmax(vmax(s[qb][0][3], s[qb][1][0]), s[qb][1][1]),
+                                   vmax(vmax(s[qb][1][2], s[qb][1][3]), -INFINITY)));
+            if (__any(tmax > m[qb] + kRescale)) {
+                tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+                tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+                const bool need = tmax > m[qb] + kRescale;
                 const float alpha = need ? __builtin_amdgcn_exp2f(m[qb] - tmax) : 1.0f;
                 m[qb] = need ? tmax : m[qb];
-                l[qb] *= alpha;
                 // acc rows are queries 4c + v: fetch their alphas from lanes 4c + v
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
                     const float av = __shfl(alpha, 4 * c + v);
+                    accl[qb][v] *= av;
 #pragma unroll
                     for (int t = 0; t < NT; ++t) acc[qb][t][v] *= av;
                 }
@@ -394,11 +458,9 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams 
 #pragma unroll
             for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    const float pv = __builtin_amdgcn_exp2f(s[qb][sub][v] - m[qb]);
-                    l[qb] += pv;
-                    pop[qb][sub * 4 + v] = (_Float16) pv;
-                }
+                for (int v = 0; v < 4; ++v)
+                    pop[qb][sub * 4 + v] = (_Float16) __builtin_amdgcn_exp2f(s[qb][sub][v] - m[qb]);
+            accl[qb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pop[qb], ones, accl[qb], 0, 0, 0);
         }
         // O += P V: B operand lane l = column t*16 + n of the tile, keys
         // 4c..4c+3 and 16+4c..16+4c+3 (the key order of pop), read with two
@@ -419,8 +481,14 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams 
     // The trip count is padded to a multiple of PF + 1 tiles (an empty tile
     // past the chunk is zeros and skipped by every wave), so the unrolled
     // body has no per-tile condition around its loads.
+    // The prologue issues its loads in the loop's order (the scheduling
+    // barriers keep hipcc from hoisting later tiles' loads), so that the
+    // loop header waits for the oldest tile only.
 #pragma unroll
-    for (int j = 0; j < PF; ++j) fetch(j, raw[j], rawd[j], rawl[j]);
+    for (int j = 0; j < PF; ++j) {
+        fetch(raw[j], rawd[j], rawl[j]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
     for (int base = 0; base < n_tiles; base += PF + 1) {
 #pragma unroll
         for (int u = 0; u <= PF; ++u) {
@@ -428,28 +496,36 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams 
             const int nxt = (u + PF) % (PF + 1);
             deposit(u & 1, raw[u], rawd[u], rawl[u]);
             lds_barrier();  // buffer u & 1 is complete; the other is free again
-            fetch(tile + PF, raw[nxt], rawd[nxt], rawl[nxt]);
+            fetch(raw[nxt], rawd[nxt], rawl[nxt]);
             compute(u & 1, k_lo + tile * kTK);
         }
     }
 
-    // Row sums of query n, then every acc row (query 4c + v) divides by its own.
+    // Every acc row (query 4c + v) divides by its weight sum; each query
+    // block goes through the wave's LDS staging and out as 16-byte row pieces.
+    float *so = reinterpret_cast<float *>(sW[wave]);
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
-        float lq = l[qb];
-        lq += __shfl_xor(lq, 16);
-        lq += __shfl_xor(lq, 32);
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-            const float lv = __shfl(lq, 4 * c + v);
-            const int qv = wq0 + qb * 16 + 4 * c + v;
-            if (qv < p.n_tok) {
-                float *orow = p.out + (((int64_t) b * p.n_tok + qv) * p.n_heads + h) * D;
-                const float inv = lv > 0.0f ? 1.0f / lv : 0.0f;
+            const float lv = accl[qb][v];
+            const float inv = lv > 0.0f ? 1.0f / lv : 0.0f;
 #pragma unroll
-                for (int t = 0; t < NT; ++t) orow[col_elem(t * 16 + n)] = acc[qb][t][v] * inv;
-            }
+            for (int t = 0; t < NT; ++t) so[(4 * c + v) * OROW + col_elem(t * 16 + n)] = acc[qb][t][v] * inv;
         }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        constexpr int CPR = D / 4;  // 16-byte pieces per output row
+#pragma unroll
+        for (int k = 0; k < 16 * CPR / 64; ++k) {
+            const int e = k * 64 + lane;
+            const int row = e / CPR, col = e % CPR;
+            const float4 x = *reinterpret_cast<const float4 *>(so + row * OROW + col * 4);
+            const int qv = wq0 + qb * 16 + row;
+            if (qv < p.n_tok)
+                *reinterpret_cast<float4 *>(p.out + (((int64_t) b * p.n_tok + qv) * p.n_heads + h) * D +
+                                            col * 4) = x;
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads done before the next block's writes
     }
 }
 
