@@ -412,10 +412,29 @@ int bmo_kv_ring_prefill(bmo_kv_ring_t *r, int layer, int n_batch, const int *ses
         if (!(scale > 0.0f)) scale = 1.0f / std::sqrt((float) r->g.head_dim);
         if (!std::isfinite(scale))
             return fail(r, BMO_ATTN_ERR_ARG, std::string(fn) + ": scale must be finite");
+        if ((int64_t) n_batch * n_tok * r->g.n_kv_heads * (r->g.head_dim / 32) * 2 > INT32_MAX)
+            return fail(r, BMO_ATTN_ERR_ARG, std::string(fn) + ": chunk too large (2^31 Q4_0 blocks)");
+        if (r->g.group_stride > (int64_t) UINT32_MAX)
+            return fail(r, BMO_ATTN_ERR_ARG,
+                        std::string(fn) + ": n_sessions * n_kv_heads too large for prefill");
         DeviceGuard dg(r->device);
         bmo::PrefillParams p{};
+        p.base = r->mem;
+        p.g = r->g;
+        p.layer = layer;
+        p.n_batch = n_batch;
+        p.n_heads = n_heads;
+        p.n_kv = r->g.n_kv_heads;
+        p.session_ids = session_ids;
+        p.pos0 = pos0;
+        p.n_tok = n_tok;
+        p.q = q;
+        p.k = k;
+        p.v = v;
+        p.out = out;
+        p.qscale = scale * kLog2e;
         p.sg = bmo::make_geom(1, n_batch, r->g.n_kv_heads, r->g.head_dim, n_tok);
-        const int64_t need = p.sg.total_bytes();
+        const int64_t need = bmo::prefill_is_direct(p) ? 0 : p.sg.total_bytes();
         if (need > r->stage_bytes) {
             // grow-only staging; the previous one may still be read by queued work
             hipError_t e = hipStreamSynchronize((hipStream_t) stream);
@@ -429,21 +448,7 @@ int bmo_kv_ring_prefill(bmo_kv_ring_t *r, int layer, int n_batch, const int *ses
             }
             r->stage_bytes = need;
         }
-        p.base = r->mem;
-        p.g = r->g;
         p.stage = r->stage;
-        p.layer = layer;
-        p.n_batch = n_batch;
-        p.n_heads = n_heads;
-        p.n_kv = r->g.n_kv_heads;
-        p.session_ids = session_ids;
-        p.pos0 = pos0;
-        p.n_tok = n_tok;
-        p.q = q;
-        p.k = k;
-        p.v = v;
-        p.out = out;
-        p.qscale = scale * kLog2e;
         if (!bmo::launch_prefill(p, (hipStream_t) stream))
             return fail(r, BMO_ATTN_ERR_ARG, std::string(fn) + ": unsupported head_dim");
         hipError_t e = hipGetLastError();

@@ -71,8 +71,6 @@ namespace {
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
-constexpr float kTwo24 = 16777216.0f;
-constexpr float kTwo20 = 1048576.0f;
 constexpr int kQMax = 30583;      // 7 * (1 + 16 + 256 + 4096): largest |Q|
 constexpr int kQBias = 34952;     // 8 * (1 + 16 + 256 + 4096)
 constexpr float kRescale = 8.0f;  // lazy rescale threshold, log2 units

@@ -72,6 +72,9 @@ bool launch_decode(const DecodeParams &p, bool fused, hipStream_t stream);
 // stage, attend, commit (three kernels in stream order); false for an
 // unsupported head_dim.
 bool launch_prefill(const PrefillParams &p, hipStream_t stream);
+// True when launch_prefill runs one attention kernel that quantizes and
+// commits the chunk itself (no staging stripes are read or written).
+bool prefill_is_direct(const PrefillParams &p);
 // Writes the zero state (ring_layout.hpp) into n_ranges ranges of
 // range_bytes bytes (a multiple of the group size) spaced range_stride apart.
 void launch_clear(uint8_t *base, int64_t range_bytes, int64_t range_stride, int n_ranges,

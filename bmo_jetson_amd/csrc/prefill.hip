@@ -123,20 +123,21 @@ __device__ __forceinline__ half8_t dequant_dword(uint32_t w, uint32_t d16) {
 
 // One thread per (row, K/V, kv head, block) of the chunk: bf16 -> fp32 ->
 // Q4_0 (the bit-exact quantizer) -> staging slot i of stripe (entry, head).
+// Thread indices fit 32 bits (the API bounds the chunk's block count).
 __global__ __launch_bounds__(256) void stage_kernel(PrefillParams p) {
     const int nblk = p.g.head_dim / kQK;
-    const int64_t per_row = (int64_t) p.n_kv * nblk * 2;
-    const int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    const int per_row = p.n_kv * nblk * 2;
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= per_row * p.n_batch * p.n_tok) return;
-    const int64_t r = t / per_row;  // b * n_tok + i
-    int rem = (int) (t % per_row);
+    const int r = t / per_row;  // b * n_tok + i
+    int rem = t - r * per_row;
     const int which = rem / (p.n_kv * nblk);
-    rem %= p.n_kv * nblk;
+    rem -= which * (p.n_kv * nblk);
     const int h = rem / nblk;
-    const int blk = rem % nblk;
-    const int b = (int) (r / p.n_tok);
-    const int i = (int) (r % p.n_tok);
-    const uint16_t *src = (which == 0 ? p.k : p.v) + (r * p.n_kv + h) * p.g.head_dim + blk * kQK;
+    const int blk = rem - h * nblk;
+    const int b = r / p.n_tok;
+    const int i = r - b * p.n_tok;
+    const uint16_t *src = (which == 0 ? p.k : p.v) + ((int64_t) r * p.n_kv + h) * p.g.head_dim + blk * kQK;
     float x[kQK];
     const uint4 *s4 = reinterpret_cast<const uint4 *>(src);
 #pragma unroll
@@ -159,16 +160,16 @@ __global__ __launch_bounds__(256) void stage_kernel(PrefillParams p) {
 // ring slot (pos0 + i) % n_ctx.  Skipped entries write nothing.
 __global__ __launch_bounds__(256) void commit_kernel(PrefillParams p) {
     const int nblk = p.g.head_dim / kQK;
-    const int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= (int64_t) p.n_batch * p.n_tok * p.n_kv * nblk) return;
-    const int blk = (int) (t % nblk);
-    const int h = (int) ((t / nblk) % p.n_kv);
-    const int i = (int) ((t / ((int64_t) nblk * p.n_kv)) % p.n_tok);
-    const int b = (int) (t / ((int64_t) nblk * p.n_kv * p.n_tok));
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= p.n_batch * p.n_tok * p.n_kv * nblk) return;
+    const int blk = t % nblk;
+    const int h = (t / nblk) % p.n_kv;
+    const int i = (t / (nblk * p.n_kv)) % p.n_tok;
+    const int b = t / (nblk * p.n_kv * p.n_tok);
     const int sid = p.session_ids ? p.session_ids[b] : b;
     const int pos0 = p.pos0[b];
-    if (sid < 0 || sid >= p.g.n_sessions || pos0 < 0) return;
-    const int slot = (int) (((int64_t) pos0 + i) % p.g.n_ctx);
+    if (sid < 0 || sid >= p.g.n_sessions || pos0 < 0 || pos0 > INT_MAX - p.n_tok) return;
+    const int slot = (pos0 + i) % p.g.n_ctx;
     const uint8_t *src = p.stage + p.sg.stripe_offset(0, b, h);
     uint8_t *dst = p.base + p.g.stripe_offset(p.layer, sid, h);
     *reinterpret_cast<uint4 *>(dst + p.g.kcode_offset(slot, blk)) =
@@ -181,7 +182,14 @@ __global__ __launch_bounds__(256) void commit_kernel(PrefillParams p) {
 
 // Eight waves per CU (two waves per SIMD): the register budget that keeps
 // the accumulators in architectural registers without spilling.
-template <int D, int QW, int QB>
+//
+// DIRECT: every (entry, kv head) stripe is read by this one workgroup (one
+// query head per kv head, the whole chunk in one workgroup).  The workgroup
+// then quantizes its chunk's K/V itself into LDS (the staging stripe's role),
+// reads the chunk's keys from there, and writes the chunk's blocks into the
+// ring after its last tile, when no wave reads the old slots any more; no
+// stage or commit kernel runs.
+template <int D, int QW, int QB, bool DIRECT>
 __global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams p) {
     constexpr int NBLK = D / kQK;
     // LDS rows (fp16): K rows padded to 68 dwords so that the 16 lanes of an
@@ -210,6 +218,10 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams 
     __shared__ __align__(16) _Float16 sK[2][kTK * KROW];
     __shared__ __align__(16) _Float16 sV[2][kTK * VROW];
     __shared__ __align__(16) uint4 sW[QW][WSTAGE];
+    // DIRECT: the chunk's blocks in ring format: codes [K/V][token][block]
+    // (K as code ^ 8), scale dwords [token][block] (K low half, V high)
+    __shared__ __align__(16) uint4 sCc[DIRECT ? 2 * QT * NBLK : 1];
+    __shared__ __align__(16) uint32_t sCs[DIRECT ? QT * NBLK : 1];
 
     const int lane = threadIdx.x & 63;
     // wave-uniform (readfirstlane), so that everything derived from it --
@@ -281,11 +293,13 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams 
         for (int j = 0; j < IPT; ++j) {
             const int t = ft[j];
             // chunk keys come from the staging stripe (slot t - pos0); older
-            // keys, and keys past the chunk (not live), from the ring
+            // keys, and keys past the chunk (not live), from the ring.  DIRECT:
+            // chunk keys come from LDS at deposit; the load reads the ring
+            // stripe's slot 0 (cached), which keeps the load count uniform.
             const bool chunk = t >= pos0 && t <= p_last;
-            const int slot = chunk ? t - pos0 : fslot[j];
-            const uint8_t *gp = (chunk ? stage : ring) +
-                                (uint64_t) (uint32_t) (slot / G) * (chunk ? stage_gs : ring_gs);
+            const int slot = chunk ? (DIRECT ? 0 : t - pos0) : fslot[j];
+            const uint8_t *gp = (chunk && !DIRECT ? stage : ring) +
+                                (uint64_t) (uint32_t) (slot / G) * (chunk && !DIRECT ? stage_gs : ring_gs);
             const uint32_t row = (uint32_t) (slot % G);
             rw[j] = *reinterpret_cast<const uint2 *>(gp + row * (D / 2) + it_code[j]);
             // the whole scale dword: a 16-bit load would be zero-extended
@@ -301,7 +315,7 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams 
     // Dequantizes fetched items into LDS buffer `buf`: K and V row-major,
     // the values of code dword cd at slots 8cd..8cd+7 of the block (the order
     // the query operand uses; col_elem maps a column back to its element).
-    auto deposit = [&](int buf, const uint2 (&rw)[IPT], const uint32_t (&rd)[IPT],
+    auto deposit = [&](int buf, int t0, const uint2 (&rw)[IPT], const uint32_t (&rd)[IPT],
                        const bool (&rl)[IPT]) {
 #pragma unroll
         for (int j = 0; j < IPT; ++j) {
@@ -311,11 +325,22 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams 
                 const int bb = (it >> 1) % NBLK;
                 const int key = it_key[j];
                 const int which = it / (2 * kTK * NBLK);
+                uint2 w = rw[j];
+                uint32_t sd = rd[j];
+                if constexpr (DIRECT) {
+                    // chunk token i of this key, if any: its blocks are in LDS
+                    const int i = t0 + key - pos0;
+                    const int ic = min(max(i, 0), QT - 1);
+                    const uint2 cw = reinterpret_cast<const uint2 *>(&sCc[(which * QT + ic) * NBLK + bb])[hf];
+                    const uint32_t cs = sCs[ic * NBLK + bb];
+                    w = i >= 0 ? cw : w;
+                    sd = i >= 0 ? cs : sd;
+                }
                 const uint32_t flip = which == 0 ? 0x88888888u : 0u;  // K codes are stored as code ^ 8
-                const uint32_t dw = which == 0 ? rd[j] & 0xFFFFu : rd[j] >> 16;
+                const uint32_t dw = which == 0 ? sd & 0xFFFFu : sd >> 16;
                 const uint32_t d16 = rl[j] ? dw : 0u;  // scale 0 past the chunk
-                const half8_t v0 = dequant_dword(rw[j].x ^ flip, d16);
-                const half8_t v1 = dequant_dword(rw[j].y ^ flip, d16);
+                const half8_t v0 = dequant_dword(w.x ^ flip, d16);
+                const half8_t v1 = dequant_dword(w.y ^ flip, d16);
                 _Float16 *dst = which == 0 ? &sK[buf][key * KROW + bb * kQK + 16 * hf]
                                            : &sV[buf][key * VROW + bb * kQK + 16 * hf];
                 *reinterpret_cast<half8_t *>(dst) = v0;
@@ -489,15 +514,78 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams 
         fetch(raw[j], rawd[j], rawl[j]);
         __builtin_amdgcn_sched_barrier(0);
     }
+    if constexpr (DIRECT) {
+        // the chunk's K and V blocks (bf16 -> Q4_0, the append quantizer)
+        // into LDS in ring format; the barrier publishes them
+        constexpr int NQ = (2 * QT * NBLK + NTHR - 1) / NTHR;
+        const int nblocks = 2 * p.n_tok * NBLK;
+        uint4 braw[NQ][4];  // this thread's blocks as loaded (bf16), all loads in flight at once
+#pragma unroll
+        for (int k = 0; k < NQ; ++k) {
+            const int e = min((int) threadIdx.x + k * NTHR, nblocks - 1);
+            const int bb = e % NBLK;
+            const int i = (e / NBLK) % p.n_tok;
+            const int which = e / (NBLK * p.n_tok);
+            const uint4 *src = reinterpret_cast<const uint4 *>(
+                (which == 0 ? p.k : p.v) + (((int64_t) b * p.n_tok + i) * p.n_kv + kvh) * D + bb * kQK);
+#pragma unroll
+            for (int cq = 0; cq < 4; ++cq) braw[k][cq] = src[cq];
+        }
+#pragma unroll
+        for (int k = 0; k < NQ; ++k) {
+            const int e = min((int) threadIdx.x + k * NTHR, nblocks - 1);
+            const int bb = e % NBLK;
+            const int i = (e / NBLK) % p.n_tok;
+            const int which = e / (NBLK * p.n_tok);
+            float x[kQK];
+#pragma unroll
+            for (int cq = 0; cq < 4; ++cq) {
+                const uint4 u = braw[k][cq];
+                const uint32_t wv[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) {
+                    x[8 * cq + 2 * jj] = bf16_to_f32(wv[jj] & 0xFFFFu);
+                    x[8 * cq + 2 * jj + 1] = bf16_to_f32(wv[jj] >> 16);
+                }
+            }
+            uint16_t d16;
+            uint32_t qs[4];
+            quantize_block_q4_0(x, d16, qs);
+            if ((int) threadIdx.x + k * NTHR < nblocks) {
+                const uint32_t flip = which == 0 ? 0x88888888u : 0u;
+                sCc[(which * QT + i) * NBLK + bb] = make_uint4(qs[0] ^ flip, qs[1] ^ flip, qs[2] ^ flip, qs[3] ^ flip);
+                reinterpret_cast<uint16_t *>(&sCs[i * NBLK + bb])[which] = d16;
+            }
+        }
+        lds_barrier();
+    }
     for (int base = 0; base < n_tiles; base += PF + 1) {
 #pragma unroll
         for (int u = 0; u <= PF; ++u) {
             const int tile = base + u;
             const int nxt = (u + PF) % (PF + 1);
-            deposit(u & 1, raw[u], rawd[u], rawl[u]);
+            deposit(u & 1, k_lo + tile * kTK, raw[u], rawd[u], rawl[u]);
             lds_barrier();  // buffer u & 1 is complete; the other is free again
             fetch(raw[nxt], rawd[nxt], rawl[nxt]);
             compute(u & 1, k_lo + tile * kTK);
+        }
+    }
+
+    if constexpr (DIRECT) {
+        // The chunk's blocks into their ring slots (pos0 + i) % n_ctx.  Every
+        // wave of this workgroup has passed the last tile's barrier, which
+        // follows the last dequantization of ring data, so no wave still
+        // needs an old slot; no other workgroup reads this stripe.  (Loads
+        // of the padding tiles past the end may still be in flight; their
+        // values are never used.)
+        uint8_t *wring = p.base + p.g.stripe_offset(p.layer, sid, kvh);
+        for (int e = threadIdx.x; e < p.n_tok * NBLK; e += NTHR) {
+            const int bb = e % NBLK;
+            const int i = e / NBLK;
+            const int slot = (pos0 + i) % n_ctx;
+            *reinterpret_cast<uint4 *>(wring + p.g.kcode_offset(slot, bb)) = sCc[i * NBLK + bb];
+            *reinterpret_cast<uint4 *>(wring + p.g.vcode_offset(slot, bb)) = sCc[(QT + i) * NBLK + bb];
+            *reinterpret_cast<uint32_t *>(wring + p.g.scale_offset(slot, bb)) = sCs[i * NBLK + bb];
         }
     }
 
@@ -529,33 +617,56 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams 
     }
 }
 
-bool launch_prefill(const PrefillParams &p, hipStream_t stream) {
-    const int nblk = p.g.head_dim / kQK;
-    const int64_t stage_threads = (int64_t) p.n_batch * p.n_tok * p.n_kv * nblk * 2;
-    hipLaunchKernelGGL(stage_kernel, dim3((unsigned) ((stage_threads + 255) / 256)), dim3(256), 0,
-                       stream, p);
-    // 32 queries per wave; 8 waves (256 queries, one workgroup per chunk of
-    // a head) or 4.  BMO_PREFILL_WAVES = 4 | 8 overrides (tuning).
+namespace {
+
+// 32 queries per wave; 8 waves (256 queries, one workgroup per chunk of a
+// head) or 4.  BMO_PREFILL_WAVES = 4 | 8 overrides (tuning).
+int prefill_waves(const PrefillParams &p) {
     int qw = p.n_tok > 128 ? 8 : 4;
     if (const char *e = std::getenv("BMO_PREFILL_WAVES")) qw = std::atoi(e) == 4 ? 4 : 8;
+    return qw;
+}
+
+template <int D, int QW, bool DIRECT>
+void launch_attention(const PrefillParams &p, dim3 grid, hipStream_t stream) {
+    hipLaunchKernelGGL((prefill_kernel<D, QW, 2, DIRECT>), grid, dim3(64 * QW), 0, stream, p);
+}
+
+template <int D>
+void launch_attention(const PrefillParams &p, int qw, bool direct, dim3 grid, hipStream_t stream) {
+    if (qw == 8)
+        direct ? launch_attention<D, 8, true>(p, grid, stream) : launch_attention<D, 8, false>(p, grid, stream);
+    else
+        direct ? launch_attention<D, 4, true>(p, grid, stream) : launch_attention<D, 4, false>(p, grid, stream);
+}
+
+}  // namespace
+
+bool prefill_is_direct(const PrefillParams &p) {
+    return p.n_heads == p.n_kv && p.n_tok <= 32 * prefill_waves(p);
+}
+
+bool launch_prefill(const PrefillParams &p, hipStream_t stream) {
+    if (p.g.head_dim != 128 && p.g.head_dim != 64) return false;
+    const int nblk = p.g.head_dim / kQK;
+    const bool direct = prefill_is_direct(p);
+    if (!direct) {
+        const int stage_threads = p.n_batch * p.n_tok * p.n_kv * nblk * 2;
+        hipLaunchKernelGGL(stage_kernel, dim3((unsigned) ((stage_threads + 255) / 256)), dim3(256), 0,
+                           stream, p);
+    }
+    const int qw = prefill_waves(p);
     const int qt = 32 * qw;
     const dim3 grid((unsigned) ((int64_t) p.n_batch * p.n_heads * ((p.n_tok + qt - 1) / qt)));
-    if (p.g.head_dim == 128) {
-        if (qw == 8)
-            hipLaunchKernelGGL((prefill_kernel<128, 8, 2>), grid, dim3(512), 0, stream, p);
-        else
-            hipLaunchKernelGGL((prefill_kernel<128, 4, 2>), grid, dim3(256), 0, stream, p);
-    } else if (p.g.head_dim == 64) {
-        if (qw == 8)
-            hipLaunchKernelGGL((prefill_kernel<64, 8, 2>), grid, dim3(512), 0, stream, p);
-        else
-            hipLaunchKernelGGL((prefill_kernel<64, 4, 2>), grid, dim3(256), 0, stream, p);
-    } else {
-        return false;
+    if (p.g.head_dim == 128)
+        launch_attention<128>(p, qw, direct, grid, stream);
+    else
+        launch_attention<64>(p, qw, direct, grid, stream);
+    if (!direct) {
+        const int commit_threads = p.n_batch * p.n_tok * p.n_kv * nblk;
+        hipLaunchKernelGGL(commit_kernel, dim3((unsigned) ((commit_threads + 255) / 256)), dim3(256), 0,
+                           stream, p);
     }
-    const int64_t commit_threads = (int64_t) p.n_batch * p.n_tok * p.n_kv * nblk;
-    hipLaunchKernelGGL(commit_kernel, dim3((unsigned) ((commit_threads + 255) / 256)), dim3(256), 0,
-                       stream, p);
     return true;
 }
 

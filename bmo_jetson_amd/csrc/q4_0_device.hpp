@@ -42,9 +42,11 @@ __device__ __forceinline__ int x86_trunc_to_i8(float s) {
 //   +0.0f; d = max / -8; id = d ? 1/d : 0; scale stored as fp16(d);
 //   code = min(15, (int8_t)(x*id + 8.5f)) with separately rounded multiply
 //   and add.  d16 receives the fp16 scale bits and qs[c] bytes 4c..4c+3 of
-//   the block (byte j = code j | code j+16 << 4).
-__device__ __forceinline__ void quantize_block_q4_0(const float (&x)[kQK], uint16_t &d16,
-                                                    uint32_t (&qs)[4]) {
+//   the block (byte j = code j | code j+16 << 4).  This is the literal form,
+//   exact for every input (NaN, infinities, scales whose reciprocal
+//   overflows).
+__device__ __forceinline__ void quantize_block_q4_0_literal(const float (&x)[kQK], uint16_t &d16,
+                                                            uint32_t (&qs)[4]) {
 #pragma clang fp contract(off)
     float amax = 0.0f;
     float vmax = 0.0f;
@@ -74,6 +76,58 @@ __device__ __forceinline__ void quantize_block_q4_0(const float (&x)[kQK], uint1
             c1 = c1 > 15 ? 15 : c1;
             const uint32_t byte = ((uint32_t) c0 | ((uint32_t) c1 << 4)) & 0xFFu;
             w |= byte << (8 * i);
+        }
+        qs[c] = w;
+    }
+}
+
+// The same function, with a short path for the common block: the largest
+// magnitude comes from NaN-propagating max/min trees (v_maximum3/v_minimum3),
+// and the sign of the first value of that magnitude is the sign of whichever
+// extreme reaches it (a scan settles blocks holding both +max and -max).
+// With no NaN, no infinity and |max| >= 2^-124 (so 1/d is finite and
+// |x*id| <= 8 up to rounding) or |max| == 0, x*id + 8.5f lies in [0, 17):
+// the truncation is the plain conversion and only the clamp to 15 remains.
+// Other blocks take the literal form.
+__device__ __forceinline__ void quantize_block_q4_0(const float (&x)[kQK], uint16_t &d16,
+                                                    uint32_t (&qs)[4]) {
+#pragma clang fp contract(off)
+    float hi = x[0], lo = x[0];
+#pragma unroll
+    for (int j = 1; j < kQK; ++j) {
+        hi = __builtin_elementwise_maximum(hi, x[j]);
+        lo = __builtin_elementwise_minimum(lo, x[j]);
+    }
+    const float amax = __builtin_elementwise_maximum(hi, -lo);  // NaN if any x is NaN
+    if (!(amax <= 3.40282347e38f && (amax >= 0x1p-124f || amax == 0.0f))) {
+        quantize_block_q4_0_literal(x, d16, qs);
+        return;
+    }
+    float vmax;
+    if (hi == amax && lo == -amax && amax != 0.0f) {
+        // both signs reach |max|: the first occurrence decides
+        vmax = 0.0f;
+#pragma unroll
+        for (int j = kQK - 1; j >= 0; --j) vmax = __builtin_fabsf(x[j]) == amax ? x[j] : vmax;
+    } else {
+        vmax = hi == amax ? amax : -amax;
+    }
+    vmax = amax == 0.0f ? 0.0f : vmax;  // an all-zero block keeps the initial +0
+    float d = vmax / -8.0f;
+    asm volatile("" : "+v"(d));  // materialize d in fp32 (see the header note)
+    const float id = (d != 0.0f) ? 1.0f / d : 0.0f;
+    d16 = f32_to_f16_bits(d);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int j = 4 * c + i;
+            int c0 = (int) (x[j] * id + 8.5f);
+            int c1 = (int) (x[j + 16] * id + 8.5f);
+            c0 = c0 > 15 ? 15 : c0;
+            c1 = c1 > 15 ? 15 : c1;
+            w |= ((uint32_t) c0 | ((uint32_t) c1 << 4)) << (8 * i);
         }
         qs[c] = w;
     }
