@@ -292,14 +292,17 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams 
 #pragma unroll
         for (int j = 0; j < IPT; ++j) {
             const int t = ft[j];
-            // chunk keys come from the staging stripe (slot t - pos0); older
-            // keys, and keys past the chunk (not live), from the ring.  DIRECT:
-            // chunk keys come from LDS at deposit; the load reads the ring
-            // stripe's slot 0 (cached), which keeps the load count uniform.
-            const bool chunk = t >= pos0 && t <= p_last;
-            const int slot = chunk ? (DIRECT ? 0 : t - pos0) : fslot[j];
-            const uint8_t *gp = (chunk && !DIRECT ? stage : ring) +
-                                (uint64_t) (uint32_t) (slot / G) * (chunk && !DIRECT ? stage_gs : ring_gs);
+            // Older keys come from the ring, chunk keys from the staging
+            // stripe (slot t - pos0), or in DIRECT mode from LDS at deposit.
+            // Loads that carry no key (DIRECT chunk keys, keys past the
+            // chunk) read the ring stripe's slot 0, which stays cached: the
+            // load count is uniform and no HBM bytes are spent on them.
+            const bool past = t > p_last;
+            const bool staged = !DIRECT && t >= pos0 && !past;
+            const bool dummy = past || (DIRECT && t >= pos0);
+            const int slot = staged ? t - pos0 : dummy ? 0 : fslot[j];
+            const uint8_t *gp = (staged ? stage : ring) +
+                                (uint64_t) (uint32_t) (slot / G) * (staged ? stage_gs : ring_gs);
             const uint32_t row = (uint32_t) (slot % G);
             rw[j] = *reinterpret_cast<const uint2 *>(gp + row * (D / 2) + it_code[j]);
             // the whole scale dword: a 16-bit load would be zero-extended

@@ -18,8 +18,8 @@
  *     call that writes slots (append, fused append+decode, write, reset,
  *     import) must be ordered with the calls that read those slots, as on one
  *     stream; decode calls alone may overlap.  Only bmo_kv_ring_create and
- *     bmo_kv_ring_prefill (its staging buffer, when a call needs a larger one
- *     than the ring holds) allocate device memory.
+ *     bmo_kv_ring_prefill (its staging buffer, when a staged call needs a
+ *     larger one than the ring holds) allocate device memory.
  *   - Functions returning int return BMO_ATTN_OK (0) or an error code below;
  *     bmo_kv_ring_last_error() then describes the most recent failure on that
  *     ring (as bmo_last_error does per handle, src/bmo_api.h:145).
@@ -175,15 +175,18 @@ BMO_ATTN_API int bmo_kv_ring_write(bmo_kv_ring_t *ring, int layer, int session,
  * stands, chunk positions from the chunk's own K/V quantized to Q4_0 exactly
  * as bmo_kv_ring_append quantizes them.  Then the chunk's blocks go to slots
  * (pos0[b]+i) % n_ctx.  The ring must hold the session's positions up to
- * pos0[b]-1 (or pos0[b] == 0).  Entries with a bad session or pos0 < 0 are
- * skipped (output zeroed, ring untouched).
+ * pos0[b]-1 (or pos0[b] == 0).  Entries with a bad session, pos0 < 0 or
+ * pos0 + n_tok > INT_MAX are skipped (output zeroed, ring untouched).  The
+ * entries of one call must name distinct sessions.
  *   q:    [n_batch][n_tok][n_heads][head_dim] bf16 (bit patterns)
  *   k, v: [n_batch][n_tok][n_kv_heads][head_dim] bf16
  *   out:  [n_batch][n_tok][n_heads][head_dim] fp32
  * Attention runs on matrix cores: K, V and the softmax weights in fp16 (K and
  * V values must lie in fp16 range, as the reference's F16 cache requires),
- * q from its bf16 values, fp32 accumulation.  Grows the ring's staging buffer
- * (n_batch * n_kv_heads stripes of n_tok slots) on first use, with a
+ * q from its bf16 values, fp32 accumulation.  With n_heads == n_kv_heads and
+ * n_tok <= 256 one kernel quantizes, attends and commits; otherwise the call
+ * stages the chunk's Q4_0 blocks in the ring's staging buffer (n_batch *
+ * n_kv_heads stripes of n_tok slots), grown on first use with a
  * synchronization of stream. */
 BMO_ATTN_API int bmo_kv_ring_prefill(bmo_kv_ring_t *ring, int layer, int n_batch,
                                      const int *session_ids, const int *pos0,

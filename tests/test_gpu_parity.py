@@ -55,6 +55,13 @@ def _adversarial_rows(n_rows, width, seed):
             x[:] = np.float32(rng.random() + 0.5) * np.sign(x)  # constant magnitude
         elif k == 10:
             x *= np.float32(2.0 ** rng.integers(-30, -14))     # fp16-subnormal scales
+        elif k == 11:
+            # non-finite values take the quantizer's literal path: a NaN is
+            # never the max and codes as 0; an infinity gives an infinite d
+            sel = rng.integers(4)
+            x[rng.integers(32)] = (np.nan, np.inf, -np.inf, np.nan)[sel]
+            if sel == 3:
+                x *= np.float32(2.0 ** -123)                   # with a near-boundary scale
     return blocks.reshape(n_rows, width)
 
 
