@@ -168,6 +168,8 @@ def bench_b1(torch, iters=200):
     res = {}
     calls = {
         "fused": lambda st: ring.append_decode(0, pos, q, k, v, out, H, stream=st),
+        "fused_rope": lambda st: ring.append_decode(0, pos, q, k, v, out, H, stream=st,
+                                                    rope_theta=10000.0),
         "decode": lambda st: ring.decode(0, pos, q, out, H, stream=st),
     }
     for name, fn in calls.items():
@@ -190,6 +192,7 @@ def bench_b1(torch, iters=200):
         "workload": "cfg1: S=1 L=1 H=32 D=128 W=512 pos=700",
         "us_per_layer_fused_graph": res["fused"]["graph_us"],
         "us_per_layer_fused_eager": res["fused"]["eager_us"],
+        "us_per_layer_fused_rope_graph": res["fused_rope"]["graph_us"],
         "us_per_layer_decode_graph": res["decode"]["graph_us"],
         "us_per_layer_decode_eager": res["decode"]["eager_us"],
         "decode_GBps_graph": round(b / (res["decode"]["graph_us"] * 1e-6) / 1e9, 1),

@@ -307,7 +307,7 @@ int bmo_kv_ring_append(bmo_kv_ring_t *r, int layer, int n_batch, const int *sess
 static int decode_common(bmo_kv_ring_t *r, const char *fn, bool fused, int layer, int n_batch,
                          const int *session_ids, const int *pos, int n_heads, const float *q,
                          const float *k_new, const float *v_new, float *out, float scale,
-                         void *stream) {
+                         float rope_theta, void *stream) {
     if (!r) return BMO_ATTN_ERR_NULL;
     try {
         if (!pos || !q || !out || (fused && (!k_new || !v_new)))
@@ -321,8 +321,12 @@ static int decode_common(bmo_kv_ring_t *r, const char *fn, bool fused, int layer
         if (!(scale > 0.0f)) scale = 1.0f / std::sqrt((float) r->g.head_dim);
         if (!std::isfinite(scale))
             return fail(r, BMO_ATTN_ERR_ARG, std::string(fn) + ": scale must be finite");
+        if (rope_theta != 0.0f && !(rope_theta > 0.0f && std::isfinite(rope_theta)))
+            return fail(r, BMO_ATTN_ERR_ARG, std::string(fn) + ": rope_theta must be positive and finite");
         DeviceGuard dg(r->device);
         bmo::DecodeParams p{};
+        p.rope = rope_theta != 0.0f;
+        p.rope_r = p.rope ? std::pow((double) rope_theta, -2.0 / (double) r->g.head_dim) : 0.0;
         p.base = r->mem;
         p.g = r->g;
         p.layer = layer;
@@ -351,14 +355,24 @@ int bmo_kv_ring_decode(bmo_kv_ring_t *r, int layer, int n_batch, const int *sess
                        const int *pos, int n_heads, const float *q, float *out, float scale,
                        void *stream) {
     return decode_common(r, "bmo_kv_ring_decode", false, layer, n_batch, session_ids, pos, n_heads,
-                         q, nullptr, nullptr, out, scale, stream);
+                         q, nullptr, nullptr, out, scale, 0.0f, stream);
 }
 
 int bmo_kv_ring_append_decode(bmo_kv_ring_t *r, int layer, int n_batch, const int *session_ids,
                               const int *pos, int n_heads, const float *q, const float *k_new,
                               const float *v_new, float *out, float scale, void *stream) {
     return decode_common(r, "bmo_kv_ring_append_decode", true, layer, n_batch, session_ids, pos,
-                         n_heads, q, k_new, v_new, out, scale, stream);
+                         n_heads, q, k_new, v_new, out, scale, 0.0f, stream);
+}
+
+int bmo_kv_ring_append_decode_rope(bmo_kv_ring_t *r, int layer, int n_batch,
+                                   const int *session_ids, const int *pos, int n_heads,
+                                   const float *q, const float *k_new, const float *v_new,
+                                   float *out, float scale, float rope_theta, void *stream) {
+    if (r && !(rope_theta > 0.0f))
+        return fail(r, BMO_ATTN_ERR_ARG, "bmo_kv_ring_append_decode_rope: rope_theta must be positive");
+    return decode_common(r, "bmo_kv_ring_append_decode_rope", true, layer, n_batch, session_ids,
+                         pos, n_heads, q, k_new, v_new, out, scale, rope_theta, stream);
 }
 
 int bmo_kv_ring_write(bmo_kv_ring_t *r, int layer, int session, int64_t pos0, int n_tok,

@@ -149,19 +149,55 @@ struct Scorer {
     }
 };
 
+// Interleaved RoPE (src/bmo_cuda_kernels.cu:317-354): pair (x[2i], x[2i+1])
+// of a head turns by pos * theta^(-2i/head_dim).  Lane i < D/2 of a wave
+// writes cos and sin (fp32) of pair i to tab: the frequency r^i by binary
+// powers of r = theta^(-2/D) and the angle, cosine and sine in double, so
+// the table is the exact rotation rounded once (the reference evaluates it
+// with fp32 fast intrinsics).
+template <int D>
+__device__ __forceinline__ void rope_table(int pos, double r, int lane, float2 *tab) {
+    if (lane < D / 2) {
+        double f = 1.0, b = r;
+        for (int i = lane; i; i >>= 1) {
+            if (i & 1) f *= b;
+            b *= b;
+        }
+        double sn, cs;
+        sincos((double) pos * f, &sn, &cs);
+        tab[lane] = make_float2((float) cs, (float) sn);
+    }
+}
+
+// (a, b) rotated by (c, s) = tab entry, every product and sum rounded.
+__device__ __forceinline__ void rope_pair(float &a, float &b, float2 cs) {
+    const float ac = a * cs.x, bs = b * cs.y, as = a * cs.y, bc = b * cs.x;
+    a = ac - bs;
+    b = as + bc;
+}
+
 // One wave turns the query row of its unit into the Scorer digit planes of
 // every block: lane l makes dword c = l % 4 of plane i = (l / 4) % 4 of block
 // (l / 16) % LPK, which holds the digits of elements 4c..4c+3 (low nibbles)
 // and 4c+16..4c+19 (high nibbles).  Results go to this wave's LDS slice.
 template <int D>
 __device__ __forceinline__ void prep_digits(const float *__restrict__ qrow, float qscale, int lane,
-                                            uint32_t *s_dig, float *s_sq) {
+                                            uint32_t *s_dig, float *s_sq, const float2 *rope) {
     constexpr int LPK = D / kQK;
     const int blk = (lane >> 4) % LPK;
     const int i = (lane >> 2) & 3;
     const int c = lane & 3;
-    const float4 lo = *reinterpret_cast<const float4 *>(qrow + blk * kQK + 4 * c);
-    const float4 hi = *reinterpret_cast<const float4 *>(qrow + blk * kQK + 4 * c + 16);
+    float4 lo = *reinterpret_cast<const float4 *>(qrow + blk * kQK + 4 * c);
+    float4 hi = *reinterpret_cast<const float4 *>(qrow + blk * kQK + 4 * c + 16);
+    if (rope) {
+        // elements 4c..4c+3 and 4c+16..4c+19 of the block are pairs
+        // blk*16 + 2c, +1 and blk*16 + 2c + 8, +9
+        const int j = blk * 16 + 2 * c;
+        rope_pair(lo.x, lo.y, rope[j]);
+        rope_pair(lo.z, lo.w, rope[j + 1]);
+        rope_pair(hi.x, hi.y, rope[j + 8]);
+        rope_pair(hi.z, hi.w, rope[j + 9]);
+    }
     const float x[8] = {lo.x * qscale, lo.y * qscale, lo.z * qscale, lo.w * qscale,
                         hi.x * qscale, hi.y * qscale, hi.z * qscale, hi.w * qscale};
     float amax = 0.0f;
@@ -231,6 +267,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     __shared__ float s_m[NW];
     __shared__ float s_l[NW];
     __shared__ float s_sq[NW][4];
+    __shared__ float2 s_rope[NW][D / 2];
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -283,7 +320,9 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
 #pragma unroll
     for (int j = 0; j < NB - 1; ++j) load_clamped(j, buf[j]);
 
-    prep_digits<D>(p.q + (int64_t) unit * D, p.qscale, lane, s_dig[wave], s_sq[wave]);
+    if (p.rope) rope_table<D>(pos, p.rope_r, lane, s_rope[wave]);  // wave-private LDS
+    prep_digits<D>(p.q + (int64_t) unit * D, p.qscale, lane, s_dig[wave], s_sq[wave],
+                   p.rope ? s_rope[wave] : nullptr);
     __syncthreads();
     Scorer score;
 #pragma unroll
@@ -320,6 +359,10 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
                                    ((int64_t) b * p.n_kv + kvh) * D + blk * kQK;
                 float x[kQK];
                 load_block_f32(src, x);
+                if (p.rope && kk == 0) {
+#pragma unroll
+                    for (int m = 0; m < kQK / 2; ++m) rope_pair(x[2 * m], x[2 * m + 1], s_rope[0][blk * 16 + m]);
+                }
                 uint16_t d;
                 quantize_block_q4_0(x, d, qs);
                 d16 = d;

@@ -43,6 +43,8 @@ struct DecodeParams {
     const float *v_new;
     float *out;          // [n_batch][n_heads][head_dim]
     float qscale;        // softmax scale * log2(e)
+    int rope;            // nonzero: rotate q (and the fused k_new) by interleaved RoPE at pos
+    double rope_r;       // theta^(-2/head_dim): pair i turns by pos * rope_r^i
 };
 
 // Chunked prefill of n_tok tokens per batch entry (prefill.hip).

@@ -133,11 +133,19 @@ class KVRing:
             float(scale), _stream(stream)))
 
     def append_decode(self, layer: int, pos, q, k, v, out, n_heads: int, session_ids=None,
-                      scale: float = 0.0, n_batch=None, stream=None):
+                      scale: float = 0.0, n_batch=None, stream=None, rope_theta: float | None = None):
+        """Fused append + attention.  With rope_theta, q and k are the pre-RoPE
+        rows and interleaved RoPE at each entry's position is applied first
+        (bmo_kv_ring_append_decode_rope)."""
         n = self._batch(pos, n_batch)
-        self._check("bmo_kv_ring_append_decode", lib().bmo_kv_ring_append_decode(
-            self._h, layer, n, _ptr(session_ids), _ptr(pos), n_heads, _ptr(q), _ptr(k), _ptr(v),
-            _ptr(out), float(scale), _stream(stream)))
+        if rope_theta is None:
+            self._check("bmo_kv_ring_append_decode", lib().bmo_kv_ring_append_decode(
+                self._h, layer, n, _ptr(session_ids), _ptr(pos), n_heads, _ptr(q), _ptr(k), _ptr(v),
+                _ptr(out), float(scale), _stream(stream)))
+        else:
+            self._check("bmo_kv_ring_append_decode_rope", lib().bmo_kv_ring_append_decode_rope(
+                self._h, layer, n, _ptr(session_ids), _ptr(pos), n_heads, _ptr(q), _ptr(k), _ptr(v),
+                _ptr(out), float(scale), float(rope_theta), _stream(stream)))
 
     def write(self, layer: int, session: int, pos0: int, k, v, n_tok=None, stream=None):
         if n_tok is None:

@@ -166,6 +166,22 @@ BMO_ATTN_API int bmo_kv_ring_write(bmo_kv_ring_t *ring, int layer, int session,
                                    int64_t pos0, int n_tok, const float *k,
                                    const float *v, void *stream);
 
+/* bmo_kv_ring_append_decode with RoPE fused in front (the rotation the
+ * reference launches separately on q and k before attention,
+ * src/bmo_cuda_kernels.cu:317-368, called at src/bmo_compute.cpp:2329-2330):
+ * q and k_new are the pre-RoPE rows; in every head, pair (x[2i], x[2i+1])
+ * turns by pos[b] * rope_theta^(-2i/head_dim) (rope_theta > 0; the model's
+ * rope_theta, default 10000, src/bmo.cpp:301-303).  The ring receives the
+ * rotated K, as the reference's cache does.  The cosine and sine are the
+ * exact values rounded to fp32 (the reference uses fp32 fast intrinsics);
+ * v_new is not rotated. */
+BMO_ATTN_API int bmo_kv_ring_append_decode_rope(bmo_kv_ring_t *ring, int layer, int n_batch,
+                                                const int *session_ids, const int *pos,
+                                                int n_heads, const float *q,
+                                                const float *k_new, const float *v_new,
+                                                float *out, float scale, float rope_theta,
+                                                void *stream);
+
 /* Chunked prefill (multi-token attention node of the reference's lazy path,
  * src/bmo_compute.cpp:2376-2418, here over the ring with a causal +
  * sliding-window mask).  Entry b writes n_tok tokens at positions pos0[b] ..

@@ -52,6 +52,9 @@ def lib() -> ctypes.CDLL:
             "orc_ring_decode_f64": (None, [P, P, i32, i32, i32, i32, i64, P, f64, P]),
             "orc_ring_prefill_f64": (None, [P, P, i32, i32, i32, i32, i64, i32, P, P, P, f64, P]),
             "orc_ring_copy_k_f32": (None, [P, i32, i32, i32, i32, i32, P]),
+            "orc_rope_freq": (f64, [f64, i32]),
+            "orc_rope_cos_sin": (None, [i32, i64, f64, P, P]),
+            "orc_rope_interleaved": (None, [P, P, i32, i32, i64, f64]),
             "orc_mix64": (u64, [u64]),
             "orc_fill_normal": (None, [u64, u64, P, i64]),
             "orc_fill_u64": (None, [u64, u64, P, i64]),
@@ -165,6 +168,28 @@ def ring_copy_k_f32(kc, t_start: int, n_pos: int) -> np.ndarray:
     out = np.zeros((n_pos, n_kv, d), dtype=np.float32)
     lib().orc_ring_copy_k_f32(_p(kc), n_kv, d, n_ctx, t_start, n_pos, _p(out))
     return out
+
+
+# ---- RoPE -------------------------------------------------------------------
+
+def rope_freq(r: float, i: int) -> float:
+    return lib().orc_rope_freq(r, i)
+
+
+def rope_cos_sin(head_dim: int, pos: int, theta: float = 10000.0):
+    cs = np.empty(head_dim // 2, dtype=np.float32)
+    sn = np.empty(head_dim // 2, dtype=np.float32)
+    lib().orc_rope_cos_sin(head_dim, pos, theta, _p(cs), _p(sn))
+    return cs, sn
+
+
+def rope_interleaved(x: np.ndarray, pos: int, theta: float = 10000.0) -> np.ndarray:
+    """x: [..., head_dim] fp32 -> the rotated copy (interleaved pairs)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    d = x.shape[-1]
+    y = np.empty_like(x)
+    lib().orc_rope_interleaved(_p(x), _p(y), x.size // d, d, pos, theta)
+    return y
 
 
 # ---- synthetic inputs -------------------------------------------------------

@@ -41,6 +41,13 @@
  *       (new semantics; the reference's lazy path at
  *       src/bmo_compute.cpp:2376-2418 is linear and unmasked).  Pinned by the
  *       identity "prefill of C tokens == C successive decode steps".
+ *   orc_rope_interleaved / orc_rope_cos_sin / orc_rope_freq
+ *       interleaved RoPE of src/bmo_cuda_kernels.cu:317-354 (pairs (2i, 2i+1),
+ *       angle pos * theta^(-2i/head_dim)), cosine and sine in double rounded
+ *       to fp32, fp32 rotation.  Pinned by a complex-exponential evaluation
+ *       in numpy, pos = 0 identity, pair-norm preservation, composition of
+ *       rotations, and the relative-position property of rotated dot
+ *       products (tests/test_oracle_rope.py).
  *   orc_cpu_decode_f32 / orc_cpu_baseline_*
  *       timed CPU baseline: fp32 restatement of the reference's single
  *       threaded eager path src/bmo_compute.cpp:927-970 over dequantized Q4_0.
@@ -109,6 +116,16 @@ void orc_ring_prefill_f64(orc_block_q4_0 *kc, orc_block_q4_0 *vc, int n_heads,
                           int n_kv_heads, int head_dim, int n_ctx, int64_t pos0,
                           int n_tok, const float *q, const float *k,
                           const float *v, double scale, double *out);
+
+/* ---- RoPE ------------------------------------------------------------------ */
+/* r^i by binary powers (square-and-multiply from the low bit), the frequency
+ * of pair i for r = theta^(-2/head_dim). */
+double orc_rope_freq(double r, int i);
+/* cos and sin (fp32) of pos * theta^(-2i/head_dim), i < head_dim/2 <= 512. */
+void orc_rope_cos_sin(int head_dim, int64_t pos, double theta, float *cs, float *sn);
+/* y = x rotated pairwise (x, y: [n_rows][head_dim]; y may be x). */
+void orc_rope_interleaved(const float *x, float *y, int n_rows, int head_dim, int64_t pos,
+                          double theta);
 
 /* Copy slots [t_start, t_start+n_pos) of K as fp32, layout (n_pos, n_heads,
  * head_dim), as bmo_copy_k_cache_f32 does (src/bmo_api.cpp:283-332). */

@@ -61,6 +61,8 @@ def test_null_handle_paths():
     assert L.bmo_kv_ring_decode(None, 0, 1, None, None, 1, None, None, 0.0, None) == 1
     assert L.bmo_kv_ring_append_decode(None, 0, 1, None, None, 1, None, None, None, None, 0.0,
                                        None) == 1
+    assert L.bmo_kv_ring_append_decode_rope(None, 0, 1, None, None, 1, None, None, None, None,
+                                            0.0, 10000.0, None) == 1
     assert L.bmo_kv_ring_write(None, 0, 0, 0, 1, None, None, None) == 1
     assert L.bmo_kv_ring_prefill(None, 0, 1, None, None, 1, 1, None, None, None, None, 0.0,
                                  None) == 1
