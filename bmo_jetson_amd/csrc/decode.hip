@@ -180,15 +180,26 @@ __device__ __forceinline__ void rope_pair(float &a, float &b, float2 cs) {
 // every block: lane l makes dword c = l % 4 of plane i = (l / 4) % 4 of block
 // (l / 16) % LPK, which holds the digits of elements 4c..4c+3 (low nibbles)
 // and 4c+16..4c+19 (high nibbles).  Results go to this wave's LDS slice.
+// The query elements lane l works on: 4c..4c+3 and 4c+16..4c+19 of block
+// (l / 16) % LPK, c = l % 4 (loaded early, ahead of the table and quantizer
+// work of the prologue).
 template <int D>
-__device__ __forceinline__ void prep_digits(const float *__restrict__ qrow, float qscale, int lane,
+__device__ __forceinline__ void prep_load(const float *__restrict__ qrow, int lane, float4 &lo,
+                                          float4 &hi) {
+    constexpr int LPK = D / kQK;
+    const int blk = (lane >> 4) % LPK;
+    const int c = lane & 3;
+    lo = *reinterpret_cast<const float4 *>(qrow + blk * kQK + 4 * c);
+    hi = *reinterpret_cast<const float4 *>(qrow + blk * kQK + 4 * c + 16);
+}
+
+template <int D>
+__device__ __forceinline__ void prep_digits(float4 lo, float4 hi, float qscale, int lane,
                                             uint32_t *s_dig, float *s_sq, const float2 *rope) {
     constexpr int LPK = D / kQK;
     const int blk = (lane >> 4) % LPK;
     const int i = (lane >> 2) & 3;
     const int c = lane & 3;
-    float4 lo = *reinterpret_cast<const float4 *>(qrow + blk * kQK + 4 * c);
-    float4 hi = *reinterpret_cast<const float4 *>(qrow + blk * kQK + 4 * c + 16);
     if (rope) {
         // elements 4c..4c+3 and 4c+16..4c+19 of the block are pairs
         // blk*16 + 2c, +1 and blk*16 + 2c + 8, +9
@@ -320,9 +331,19 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
 #pragma unroll
     for (int j = 0; j < NB - 1; ++j) load_clamped(j, buf[j]);
 
+    float4 q_lo, q_hi;
+    prep_load<D>(p.q + (int64_t) unit * D, lane, q_lo, q_hi);
+    // Fused: wave 0's lane blk (kk == 0) holds K block blk of the current
+    // token, lane LPK + blk (kk == 1) its V block; loaded here so that their
+    // latency overlaps the query's.
+    float xnew[kQK];
+    if constexpr (FUSED) {
+        if (wave == 0 && kk < 2)
+            load_block_f32((kk == 0 ? p.k_new : p.v_new) + ((int64_t) b * p.n_kv + kvh) * D + blk * kQK,
+                           xnew);
+    }
     if (p.rope) rope_table<D>(pos, p.rope_r, lane, s_rope[wave]);  // wave-private LDS
-    prep_digits<D>(p.q + (int64_t) unit * D, p.qscale, lane, s_dig[wave], s_sq[wave],
-                   p.rope ? s_rope[wave] : nullptr);
+    prep_digits<D>(q_lo, q_hi, p.qscale, lane, s_dig[wave], s_sq[wave], p.rope ? s_rope[wave] : nullptr);
     __syncthreads();
     Scorer score;
 #pragma unroll
@@ -355,16 +376,13 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
             uint32_t qs[4] = {0u, 0u, 0u, 0u};
             uint32_t d16 = 0;
             if (kk < 2) {
-                const float *src = (kk == 0 ? p.k_new : p.v_new) +
-                                   ((int64_t) b * p.n_kv + kvh) * D + blk * kQK;
-                float x[kQK];
-                load_block_f32(src, x);
                 if (p.rope && kk == 0) {
 #pragma unroll
-                    for (int m = 0; m < kQK / 2; ++m) rope_pair(x[2 * m], x[2 * m + 1], s_rope[0][blk * 16 + m]);
+                    for (int m = 0; m < kQK / 2; ++m)
+                        rope_pair(xnew[2 * m], xnew[2 * m + 1], s_rope[0][blk * 16 + m]);
                 }
                 uint16_t d;
-                quantize_block_q4_0(x, d, qs);
+                quantize_block_q4_0(xnew, d, qs);
                 d16 = d;
                 if (h % q_per_kv == 0) store_block(stripe, g, cur, blk, kk, d, qs);
             }
