@@ -287,6 +287,48 @@ def bench_prefill(torch, reps=10):
     return res
 
 
+def bench_gemv(torch, reps=50):
+    """SURVEY next row 2: the Q4_0 x Q8_1 GEMV around attention, at the
+    reference's bench shapes (src/bmo_kernel_bench.cu:387-389) and the output
+    projection, x = 0.5 as in the reference bench.  Per call from HIP-graph
+    replays; GB/s counts the Q4_0 weight bytes (18 per 32 elements)."""
+    import ctypes
+    from bmo_jetson_amd import _lib
+    res = {}
+    L = _lib.lib()
+    for name, rows, cols in (("qkv_12288x4096", 12288, 4096), ("out_4096x4096", 4096, 4096),
+                             ("gate_in_11264x4096", 11264, 4096), ("gate_out_4096x5632", 4096, 5632)):
+        nbytes = rows * cols // 32 * 18
+        # enough weight copies that one graph's calls stream > 600 MB, so the
+        # 256 MB last-level cache cannot serve them
+        n_copies = -(-600_000_000 // nbytes)
+        w = torch.randint(0, 256, (n_copies, nbytes), dtype=torch.uint8, device="cuda")
+        # scales: finite fp16 values in [0.001, 0.06) in every block's first two bytes
+        wv = w.view(-1, 18)
+        wv[:, 0:2] = torch.empty(wv.shape[0], dtype=torch.float16, device="cuda").uniform_(
+            0.001, 0.06).view(torch.uint8).view(-1, 2)
+        x = torch.full((cols,), 0.5, device="cuda")
+        y = torch.empty(rows, device="cuda")
+        state = {"i": 0}
+
+        def call(st, w=w, x=x, y=y, rows=rows, cols=cols, n_copies=n_copies, state=state):
+            wp = w[state["i"] % n_copies]
+            state["i"] += 1
+            rc = L.bmo_launch_gemv_q4_0_q8_1(ctypes.c_void_p(wp.data_ptr()), ctypes.c_void_p(x.data_ptr()),
+                                             ctypes.c_void_p(y.data_ptr()), rows, cols, None,
+                                             ctypes.c_void_p(st.cuda_stream))
+            assert rc == 0
+
+        for _ in range(5):
+            call(torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        us = graph_us_per_call(torch, call, max(reps, n_copies))
+        del w
+        res[name] = {"us": round(us, 3), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+                     "hbm_frac": round(nbytes / (us * 1e-6) / 8e12, 4), "weight_bytes": nbytes}
+    return res
+
+
 def cpu_baseline(torch, ring, L, S, H, D, W, pos_host, q_dev, out_dev, budget_s):
     """Times the oracle's fp32 restatement of the reference CPU path
     (src/bmo_compute.cpp:927-970) on host threads over a sample of the same
@@ -346,6 +388,8 @@ def main():
     ap.add_argument("--no-b1", action="store_true")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only run the cfg5 chunked-prefill leg and print its JSON (profiling)")
+    ap.add_argument("--gemv-only", action="store_true",
+                    help="only run the Q4_0 GEMV leg and print its JSON (profiling)")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="only run a plain device copy of this size (rocprof PMC calibration)")
     args = ap.parse_args()
@@ -374,6 +418,9 @@ def main():
 
     if args.prefill_only:
         print(json.dumps({"prefill": bench_prefill(torch)}), flush=True)
+        return
+    if args.gemv_only:
+        print(json.dumps({"gemv": bench_gemv(torch)}), flush=True)
         return
 
     from bmo_jetson_amd import KVRing
@@ -462,6 +509,8 @@ def main():
         log(f"[bench] depformer: {result['depformer']}")
         result["prefill"] = bench_prefill(torch)
         log(f"[bench] prefill: {result['prefill']}")
+        result["gemv"] = bench_gemv(torch)
+        log(f"[bench] gemv: {result['gemv']}")
     if not args.no_cpu:
         log("[bench] timing the CPU baseline")
         result["cpu_baseline"] = cpu_baseline(torch, ring, L, S, H, D, W, pos_host, q, out,

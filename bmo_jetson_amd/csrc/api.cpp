@@ -587,6 +587,43 @@ int64_t bmo_kv_ring_import_q4_0(bmo_kv_ring_t *r, int layer, int session, int wh
     }
 }
 
+int bmo_launch_gemv_q4_0_q8_1(const void *W_dev, const float *x_dev, float *y_dev, int rows,
+                              int cols, void *q8_scratch, void *stream) {
+    // Same arguments as src/bmo_cuda_kernels.cu:685-711 (which returns
+    // nothing); rejected arguments launch nothing, are reported once on
+    // stderr and return an error code.
+    static bool warned = false;
+    auto reject = [](int code, const char *why) {
+        if (!warned) {
+            warned = true;
+            std::fprintf(stderr, "[bmo_attn] bmo_launch_gemv_q4_0_q8_1: %s\n", why);
+        }
+        return code;
+    };
+    try {
+        if (!W_dev || !x_dev || !y_dev) return reject(BMO_ATTN_ERR_NULL, "null pointer argument");
+        if (rows <= 0 || cols <= 0 || cols % 64 != 0)
+            return reject(BMO_ATTN_ERR_ARG, "rows must be positive and cols a positive multiple of 64");
+        if (bmo::gemv_lds_bytes(cols) > 64 * 1024)
+            return reject(BMO_ATTN_ERR_ARG, "cols too large (at most 52428)");
+        if ((reinterpret_cast<uintptr_t>(W_dev) & 3) || (reinterpret_cast<uintptr_t>(x_dev) & 15) ||
+            (reinterpret_cast<uintptr_t>(q8_scratch) & 3))
+            return reject(BMO_ATTN_ERR_ARG, "W_dev and q8_scratch must be 4-byte, x_dev 16-byte aligned");
+        bmo::GemvParams p{};
+        p.w = static_cast<const uint8_t *>(W_dev);
+        p.x = x_dev;
+        p.y = y_dev;
+        p.rows = rows;
+        p.cols = cols;
+        p.q8_out = static_cast<uint8_t *>(q8_scratch);
+        bmo::launch_gemv(p, (hipStream_t) stream);
+        if (hipGetLastError() != hipSuccess) return reject(BMO_ATTN_ERR_HIP, "launch failed");
+        return BMO_ATTN_OK;
+    } catch (...) {
+        return reject(BMO_ATTN_ERR_INTERNAL, "unknown exception");
+    }
+}
+
 void bmo_launch_decode_attention(const float *q_dev, const float *k_dev, const float *v_dev,
                                  void *k_cache_dev, void *v_cache_dev, float *out_dev, int head_dim,
                                  int n_heads, int n_kv_heads, int n_ctx, int n_past, int layer,

@@ -74,6 +74,18 @@ bool launch_decode(const DecodeParams &p, bool fused, hipStream_t stream);
 // stage, attend, commit (three kernels in stream order); false for an
 // unsupported head_dim.
 bool launch_prefill(const PrefillParams &p, hipStream_t stream);
+
+struct GemvParams {
+    const uint8_t *w;  // ggml block_q4_0 rows [rows][cols/32] (18 bytes each)
+    const float *x;    // [cols]
+    float *y;          // [rows]
+    int rows;
+    int cols;          // a multiple of 64
+    uint8_t *q8_out;   // nullable: the activation's Q8_1 blocks (36 bytes each)
+};
+// LDS bytes gemv_kernel needs for cols columns.
+size_t gemv_lds_bytes(int cols);
+bool launch_gemv(const GemvParams &p, hipStream_t stream);
 // True when launch_prefill runs one attention kernel that quantizes and
 // commits the chunk itself (no staging stripes are read or written).
 bool prefill_is_direct(const PrefillParams &p);

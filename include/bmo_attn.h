@@ -239,6 +239,26 @@ BMO_ATTN_API int64_t bmo_kv_ring_import_q4_0(bmo_kv_ring_t *ring, int layer,
                                              int t_start, int n_positions,
                                              const void *in, int64_t n_bytes);
 
+/* ---- Q4_0 weight GEMV (the projections around attention) -------------------- */
+
+/* Same arguments as the reference's launch_gemv_q4_0_q8_1
+ * (src/bmo_cuda_kernels.cu:685-711, the QKV projection before attention and
+ * the output projection after it, src/bmo_compute.cpp:2232,2423):
+ * y[r] = row r of W (rows x cols, ggml block_q4_0 AoS, 18 bytes per 32
+ * elements, device memory) times x (cols fp32), with x quantized to the
+ * reference's Q8_1 (d = amax/127, q = roundf(x/d) clamped, s = fp16 of the
+ * fp32 sum of the x values) and every block contributing
+ * d4 * (sum(code*q) * d8 - 8 * s8).  One launch: each workgroup quantizes x
+ * itself.  q8_scratch may be NULL; when given (cols/32 * 36 bytes) it receives
+ * the Q8_1 blocks, as the reference's scratch does.  cols must be a multiple
+ * of 64 (at most 52428); W_dev and q8_scratch 4-byte aligned, x_dev 16-byte
+ * aligned.  Asynchronous on stream.  Returns BMO_ATTN_OK or an error code;
+ * rejected arguments launch nothing and are reported once on stderr (the
+ * reference's launcher returns nothing). */
+BMO_ATTN_API int bmo_launch_gemv_q4_0_q8_1(const void *W_dev, const float *x_dev,
+                                           float *y_dev, int rows, int cols,
+                                           void *q8_scratch, void *stream);
+
 /* ---- node-level drop-in ------------------------------------------------------ */
 
 /* Same signature and semantics as the reference's launch_decode_attention

@@ -52,6 +52,10 @@ def lib() -> ctypes.CDLL:
             "orc_ring_decode_f64": (None, [P, P, i32, i32, i32, i32, i64, P, f64, P]),
             "orc_ring_prefill_f64": (None, [P, P, i32, i32, i32, i32, i64, i32, P, P, P, f64, P]),
             "orc_ring_copy_k_f32": (None, [P, i32, i32, i32, i32, i32, P]),
+            "orc_quantize_row_q8_1_bmo": (None, [P, P, i64]),
+            "orc_vec_dot_q4_0_q8_1_f64": (f64, [P, P, i64]),
+            "orc_gemv_q4_0_q8_1_f64": (None, [P, P, i32, i32, P]),
+            "orc_gemv_term_abs_f64": (None, [P, P, i32, i32, P]),
             "orc_rope_freq": (f64, [f64, i32]),
             "orc_rope_cos_sin": (None, [i32, i64, f64, P, P]),
             "orc_rope_interleaved": (None, [P, P, i32, i32, i64, f64]),
@@ -168,6 +172,30 @@ def ring_copy_k_f32(kc, t_start: int, n_pos: int) -> np.ndarray:
     out = np.zeros((n_pos, n_kv, d), dtype=np.float32)
     lib().orc_ring_copy_k_f32(_p(kc), n_kv, d, n_ctx, t_start, n_pos, _p(out))
     return out
+
+
+# ---- Q4_0 x Q8_1 GEMV -------------------------------------------------------
+
+Q8_1 = np.dtype([("d", "<u2"), ("s", "<u2"), ("qs", "i1", (32,))])
+
+
+def quantize_q8_1(x: np.ndarray) -> np.ndarray:
+    """fp32 row (multiple of 32) -> the reference's Q8_1 blocks (36 bytes each)."""
+    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    out = np.zeros(x.size // 32, dtype=Q8_1)
+    lib().orc_quantize_row_q8_1_bmo(_p(x), out.ctypes.data, x.size)
+    return out
+
+
+def gemv_q4_0_q8_1_f64(w_blocks: np.ndarray, xq: np.ndarray, rows: int, cols: int):
+    """w_blocks: [rows * cols/32] Q4_0 blocks (ggml AoS); xq: Q8_1 blocks.
+    Returns (y, term_abs), both float64 [rows]."""
+    w = np.ascontiguousarray(w_blocks)
+    y = np.zeros(rows, dtype=np.float64)
+    t = np.zeros(rows, dtype=np.float64)
+    lib().orc_gemv_q4_0_q8_1_f64(w.ctypes.data, xq.ctypes.data, rows, cols, _p(y))
+    lib().orc_gemv_term_abs_f64(w.ctypes.data, xq.ctypes.data, rows, cols, _p(t))
+    return y, t
 
 
 # ---- RoPE -------------------------------------------------------------------

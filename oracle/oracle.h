@@ -48,6 +48,13 @@
  *       in numpy, pos = 0 identity, pair-norm preservation, composition of
  *       rotations, and the relative-position property of rotated dot
  *       products (tests/test_oracle_rope.py).
+ *   orc_quantize_row_q8_1_bmo / orc_gemv_q4_0_q8_1_f64
+ *       the reference's activation quantizer and Q4_0 x Q8_1 GEMV
+ *       (src/bmo_cuda_kernels.cu:529-711), terms summed in double.  Pinned
+ *       by hand-derived known answers (round half away from zero, clamp,
+ *       the sum field), nearest-code and range invariants, and an
+ *       independent numpy evaluation from the raw block bytes
+ *       (tests/test_oracle_gemv.py).
  *   orc_cpu_decode_f32 / orc_cpu_baseline_*
  *       timed CPU baseline: fp32 restatement of the reference's single
  *       threaded eager path src/bmo_compute.cpp:927-970 over dequantized Q4_0.
@@ -116,6 +123,26 @@ void orc_ring_prefill_f64(orc_block_q4_0 *kc, orc_block_q4_0 *vc, int n_heads,
                           int n_kv_heads, int head_dim, int n_ctx, int64_t pos0,
                           int n_tok, const float *q, const float *k,
                           const float *v, double scale, double *out);
+
+/* ---- Q4_0 x Q8_1 GEMV ------------------------------------------------------ */
+#define ORC_QK8_1 32
+/* 36-byte Q8_1 block, byte-identical to the reference's bmo_block_q8_1
+ * (src/bmo_cuda_kernels.cu:501-504): fp16 d, fp16 s, 32 int8. */
+typedef struct {
+    uint16_t d;
+    uint16_t s;
+    int8_t qs[ORC_QK8_1];
+} orc_block_q8_1;
+
+void orc_quantize_row_q8_1_bmo(const float *x, orc_block_q8_1 *y, int64_t k);
+double orc_vec_dot_q4_0_q8_1_f64(const orc_block_q4_0 *w, const orc_block_q8_1 *x, int64_t nb);
+/* y[r] = row r of w (rows x cols/32 blocks) dotted with x (cols/32 blocks). */
+void orc_gemv_q4_0_q8_1_f64(const orc_block_q4_0 *w, const orc_block_q8_1 *x, int rows,
+                            int cols, double *y);
+/* Sum over blocks of |d4| * (|sumi * d8| + |8 * s8|): the scale of the
+ * rounding error of any fp32 evaluation of row r (tolerance helper). */
+void orc_gemv_term_abs_f64(const orc_block_q4_0 *w, const orc_block_q8_1 *x, int rows, int cols,
+                           double *y);
 
 /* ---- RoPE ------------------------------------------------------------------ */
 /* r^i by binary powers (square-and-multiply from the low bit), the frequency
