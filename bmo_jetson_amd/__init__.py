@@ -15,6 +15,8 @@ from .ring import (  # noqa: F401
     KVRing,
     RingError,
     launch_decode_attention,
+    positions_advance,
+    gemv_q4_0_q8_1,
     stripe_bytes,
     BLOCK_Q4_0_BYTES,
 )
@@ -23,6 +25,8 @@ __all__ = [
     "KVRing",
     "RingError",
     "launch_decode_attention",
+    "positions_advance",
+    "gemv_q4_0_q8_1",
     "stripe_bytes",
     "BLOCK_Q4_0_BYTES",
     "lib",

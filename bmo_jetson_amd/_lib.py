@@ -34,6 +34,7 @@ SIGNATURES = {
     "bmo_kv_ring_append_decode": (i32, [P, i32, i32, P, P, i32, P, P, P, P, f32, P]),
     "bmo_kv_ring_append_decode_rope": (i32, [P, i32, i32, P, P, i32, P, P, P, P, f32, f32, P]),
     "bmo_launch_gemv_q4_0_q8_1": (i32, [P, P, P, i32, i32, P, P]),
+    "bmo_positions_advance": (i32, [P, i32, i32, P]),
     "bmo_kv_ring_write": (i32, [P, i32, i32, i64, i32, P, P, P]),
     "bmo_kv_ring_prefill": (i32, [P, i32, i32, P, P, i32, i32, P, P, P, P, f32, P]),
     "bmo_kv_ring_copy_k_f32": (i32, [P, i32, i32, i32, i32, P, i32]),

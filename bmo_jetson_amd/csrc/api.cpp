@@ -587,6 +587,13 @@ int64_t bmo_kv_ring_import_q4_0(bmo_kv_ring_t *r, int layer, int session, int wh
     }
 }
 
+int bmo_positions_advance(int *pos_dev, int n, int delta, void *stream) {
+    if (!pos_dev) return BMO_ATTN_ERR_NULL;
+    if (n <= 0) return BMO_ATTN_ERR_ARG;
+    bmo::launch_advance(pos_dev, n, delta, (hipStream_t) stream);
+    return hipGetLastError() == hipSuccess ? BMO_ATTN_OK : BMO_ATTN_ERR_HIP;
+}
+
 int bmo_launch_gemv_q4_0_q8_1(const void *W_dev, const float *x_dev, float *y_dev, int rows,
                               int cols, void *q8_scratch, void *stream) {
     // Same arguments as src/bmo_cuda_kernels.cu:685-711 (which returns

@@ -80,6 +80,18 @@ void launch_clear(uint8_t *base, int64_t range_bytes, int64_t range_stride, int 
                        range_stride, n_ranges);
 }
 
+// pos[i] += delta for i < n (positions that live in device memory, so that a
+// captured decode step advances them on every replay).
+__global__ __launch_bounds__(256) void advance_kernel(int *pos, int n, int delta) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) pos[i] += delta;
+}
+
+void launch_advance(int *pos, int n, int delta, hipStream_t stream) {
+    hipLaunchKernelGGL(advance_kernel, dim3((unsigned) ((n + 255) / 256)), dim3(256), 0, stream, pos, n,
+                       delta);
+}
+
 void launch_append(const AppendParams &p, hipStream_t stream) {
     const int nblk = p.g.head_dim / kQK;
     const int64_t threads = (int64_t) p.n_rows * p.g.n_kv_heads * nblk * 2;

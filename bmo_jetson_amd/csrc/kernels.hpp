@@ -70,6 +70,7 @@ struct PrefillParams {
 // Launchers enqueue only; they leave launch errors for the caller's
 // hipGetLastError().  launch_decode returns false for an unsupported head_dim.
 void launch_append(const AppendParams &p, hipStream_t stream);
+void launch_advance(int *pos, int n, int delta, hipStream_t stream);
 bool launch_decode(const DecodeParams &p, bool fused, hipStream_t stream);
 // stage, attend, commit (three kernels in stream order); false for an
 // unsupported head_dim.

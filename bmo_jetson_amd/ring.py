@@ -227,3 +227,20 @@ def launch_decode_attention(q, k, v, k_cache, v_cache, out, head_dim: int, n_hea
     lib().bmo_launch_decode_attention(_ptr(q), _ptr(k), _ptr(v), _ptr(k_cache), _ptr(v_cache),
                                       _ptr(out), head_dim, n_heads, n_kv_heads, n_ctx, n_past,
                                       layer, _stream(stream), _ptr(pos_dev))
+
+
+def positions_advance(pos, n: int, delta: int = 1, stream=None) -> None:
+    """pos[i] += delta on the device (capturable: a graph of a decode step
+    ending with it advances its own positions on every replay)."""
+    rc = lib().bmo_positions_advance(_ptr(pos), int(n), int(delta), _stream(stream))
+    if rc != 0:
+        raise RingError("bmo_positions_advance", rc, None)
+
+
+def gemv_q4_0_q8_1(w, x, y, rows: int, cols: int, q8_scratch=None, stream=None) -> None:
+    """y = W x for ggml Q4_0 weights W (rows x cols, device bytes) and fp32 x,
+    with x quantized to the reference's Q8_1 (bmo_launch_gemv_q4_0_q8_1)."""
+    rc = lib().bmo_launch_gemv_q4_0_q8_1(_ptr(w), _ptr(x), _ptr(y), int(rows), int(cols),
+                                         _ptr(q8_scratch), _stream(stream))
+    if rc != 0:
+        raise RingError("bmo_launch_gemv_q4_0_q8_1", rc, None)

@@ -239,6 +239,20 @@ BMO_ATTN_API int64_t bmo_kv_ring_import_q4_0(bmo_kv_ring_t *ring, int layer,
                                              int t_start, int n_positions,
                                              const void *in, int64_t n_bytes);
 
+/* ---- graph replay ----------------------------------------------------------- */
+
+/* pos_dev[i] += delta for i < n, asynchronously on stream.  Every entry point
+ * above reads positions from device memory when each kernel runs, and none
+ * allocates, synchronizes or records a memset on a decode step, so a whole
+ * step (the L layers' bmo_kv_ring_append_decode[_rope] calls followed by this
+ * advance) can be captured once into a HIP graph and replayed per token: each
+ * replay attends, appends and rotates at the current positions.  (The
+ * reference's static capture froze RoPE at the capture-time position and was
+ * disabled, src/bmo_api.cpp:334-350.)  bmo_kv_ring_prefill allocates only
+ * when a staged call needs a larger staging buffer than the ring holds; call
+ * it once eagerly before capturing it. */
+BMO_ATTN_API int bmo_positions_advance(int *pos_dev, int n, int delta, void *stream);
+
 /* ---- Q4_0 weight GEMV (the projections around attention) -------------------- */
 
 /* Same arguments as the reference's launch_gemv_q4_0_q8_1
