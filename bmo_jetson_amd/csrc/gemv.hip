@@ -101,10 +101,11 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
     int c = blockIdx.x * (NT / 64) + wave;
     int it = 0;
     uint32_t wcur[R][9];
-    load_pairs(min(c, n_chunks - 1), 0, wcur);
 
     // Activation row -> Q8_1 in LDS.  Thread t: block t/4 (+128 k), elements
-    // 8 (t%4) .. 8 (t%4) + 7.
+    // 8 (t%4) .. 8 (t%4) + 7.  The first pass's x loads go out before the
+    // weight loads: loads return in order, so the quantization then overlaps
+    // the weights' flight instead of waiting for it.
     for (int base = 0; base < nblk; base += NT / 4) {
         const int blk = base + (int) (threadIdx.x >> 2);
         const int part = threadIdx.x & 3;
@@ -112,6 +113,7 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
         const float *xb = p.x + b * 32;
         const float4 u = *reinterpret_cast<const float4 *>(xb + 8 * part);
         const float4 v = *reinterpret_cast<const float4 *>(xb + 8 * part + 4);
+        if (base == 0) load_pairs(min(c, n_chunks - 1), 0, wcur);
         const float x8[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
         float amax = 0.0f;
 #pragma unroll
@@ -126,18 +128,17 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
             const int q = min(max(round_half_away(x8[j] * id), -128), 127);
             qw[j >> 2] |= ((uint32_t) q & 0xFFu) << (8 * (j & 3));
         }
+        // the reference's sequential fp32 sum of the block's 32 values, in
+        // lane part 0, which reads its quad-mates' values through DPP
         float sum = 0.0f;
-        if (part == 0) {
-            // the reference's sequential fp32 sum of the block's 32 values
 #pragma unroll
-            for (int cq = 0; cq < 8; ++cq) {
-                const float4 t = *reinterpret_cast<const float4 *>(xb + 4 * cq);
-                sum += t.x;
-                sum += t.y;
-                sum += t.z;
-                sum += t.w;
-            }
-        }
+        for (int j = 0; j < 8; ++j) sum += x8[j];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sum += gdpp<0x55>(x8[j]);  // quad_perm [1,1,1,1]
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sum += gdpp<0xAA>(x8[j]);  // quad_perm [2,2,2,2]
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sum += gdpp<0xFF>(x8[j]);  // quad_perm [3,3,3,3]
         if (blk < nblk) {
             *reinterpret_cast<uint2 *>(sq + blk * 32 + 8 * part) = make_uint2(qw[0], qw[1]);
             const uint32_t d16 = f32_to_f16(d), s16 = f32_to_f16(sum);
