@@ -208,16 +208,14 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams 
     constexpr int G = keys_per_group(D);
     static_assert((G & (G - 1)) == 0, "slot groups are a power of two");
 
-    // Per-wave staging (wave-private): the wave's query rows (bf16) at the
-    // start, its output rows (fp32, one query block at a time) at the end, so
-    // that both move between HBM and LDS as whole 16-byte row pieces.
-    constexpr int QROW = D + 8;    // bf16 per staged query row
-    constexpr int OROW = D + 4;    // fp32 per staged output row
-    constexpr int WSTAGE = (QWV * QROW * 2 > 16 * OROW * 4 ? QWV * QROW * 2 : 16 * OROW * 4) / 16;
+    // Tiles per barrier: TPB tiles are dequantized, published by one barrier
+    // and then multiplied, through 2 * TPB LDS buffers, so the waves of a
+    // workgroup synchronize once per TPB tiles.
+    constexpr int TPB = 2;
+    constexpr int NBUF = 2 * TPB;
 
-    __shared__ __align__(16) _Float16 sK[2][kTK * KROW];
-    __shared__ __align__(16) _Float16 sV[2][kTK * VROW];
-    __shared__ __align__(16) uint4 sW[QW][WSTAGE];
+    __shared__ __align__(16) _Float16 sK[NBUF][kTK * KROW];
+    __shared__ __align__(16) _Float16 sV[NBUF][kTK * VROW];
     // DIRECT: the chunk's blocks in ring format: codes [K/V][token][block]
     // (K as code ^ 8), scale dwords [token][block] (K low half, V high)
     __shared__ __align__(16) uint4 sCc[DIRECT ? 2 * QT * NBLK : 1];
@@ -284,7 +282,7 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams 
     // on every path and the compiler's waits stay exact; the liveness flag is
     // applied at dequantization, not at the load.
     constexpr int PF = 7;
-    static_assert((PF + 1) % 2 == 0, "LDS buffer parity must follow the unrolled slot");
+    static_assert((PF + 1) % NBUF == 0, "the unrolled slot must determine the LDS buffer");
     uint2 raw[PF + 1][IPT];
     uint32_t rawd[PF + 1][IPT];
     bool rawl[PF + 1][IPT];
@@ -361,27 +359,12 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams 
     const int wq0 = i0 + wave * QWV;  // first query of this wave
     half8_t qop[QB][NBLK];
     int mrel[QB];  // this lane's query position minus 4c (mask arithmetic)
-    uint16_t *sq = reinterpret_cast<uint16_t *>(sW[wave]);
-    {
-        // the wave's QWV query rows, 16 bytes per lane and load, into LDS
-        constexpr int CPR = D / 8;  // 16-byte pieces per row
-#pragma unroll
-        for (int k = 0; k < QWV * CPR / 64; ++k) {
-            const int e = k * 64 + lane;
-            const int row = e / CPR, col = e % CPR;
-            const int qi = min(wq0 + row, p.n_tok - 1);
-            const uint4 x = *reinterpret_cast<const uint4 *>(
-                p.q + (((int64_t) b * p.n_tok + qi) * p.n_heads + h) * D + col * 8);
-            *reinterpret_cast<uint4 *>(sq + row * QROW + col * 8) = x;
-        }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // wave-private: no barrier needed
-    }
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
         const int qi = wq0 + qb * 16 + n;
         const bool q_ok = qi < p.n_tok;
         mrel[qb] = pos0 + qi - 4 * c;
-        const uint16_t *qrow = sq + (qb * 16 + n) * QROW;
+        const uint16_t *qrow = p.q + (((int64_t) b * p.n_tok + (q_ok ? qi : 0)) * p.n_heads + h) * D;
         uint2 lo[NBLK], hi[NBLK];
 #pragma unroll
         for (int bb = 0; bb < NBLK; ++bb) {
@@ -562,15 +545,24 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams 
         }
         lds_barrier();
     }
+    // Tile T lives in raw slot T % (PF + 1) and LDS buffer T % NBUF; its
+    // loads are issued PF tiles ahead, into the slot of tile T - 1.  Buffer
+    // safety: the barrier of a tile pair follows every wave's multiplication
+    // of the pair before, so writing a buffer NBUF tiles later is safe.
     for (int base = 0; base < n_tiles; base += PF + 1) {
 #pragma unroll
-        for (int u = 0; u <= PF; ++u) {
-            const int tile = base + u;
-            const int nxt = (u + PF) % (PF + 1);
-            deposit(u & 1, k_lo + tile * kTK, raw[u], rawd[u], rawl[u]);
-            lds_barrier();  // buffer u & 1 is complete; the other is free again
-            fetch(raw[nxt], rawd[nxt], rawl[nxt]);
-            compute(u & 1, k_lo + tile * kTK);
+        for (int u = 0; u <= PF; u += TPB) {
+#pragma unroll
+            for (int k = 0; k < TPB; ++k)
+                deposit((u + k) % NBUF, k_lo + (base + u + k) * kTK, raw[u + k], rawd[u + k], rawl[u + k]);
+            lds_barrier();  // these TPB buffers are complete
+#pragma unroll
+            for (int k = 0; k < TPB; ++k) {
+                const int nxt = (u + k + PF) % (PF + 1);
+                fetch(raw[nxt], rawd[nxt], rawl[nxt]);
+            }
+#pragma unroll
+            for (int k = 0; k < TPB; ++k) compute((u + k) % NBUF, k_lo + (base + u + k) * kTK);
         }
     }
 
@@ -592,31 +584,20 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams 
         }
     }
 
-    // Every acc row (query 4c + v) divides by its weight sum; each query
-    // block goes through the wave's LDS staging and out as 16-byte row pieces.
-    float *so = reinterpret_cast<float *>(sW[wave]);
+    // Every acc row (query 4c + v) divides by its weight sum.
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             const float lv = accl[qb][v];
-            const float inv = lv > 0.0f ? 1.0f / lv : 0.0f;
+            const int qv = wq0 + qb * 16 + 4 * c + v;
+            if (qv < p.n_tok) {
+                float *orow = p.out + (((int64_t) b * p.n_tok + qv) * p.n_heads + h) * D;
+                const float inv = lv > 0.0f ? 1.0f / lv : 0.0f;
 #pragma unroll
-            for (int t = 0; t < NT; ++t) so[(4 * c + v) * OROW + col_elem(t * 16 + n)] = acc[qb][t][v] * inv;
+                for (int t = 0; t < NT; ++t) orow[col_elem(t * 16 + n)] = acc[qb][t][v] * inv;
+            }
         }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        constexpr int CPR = D / 4;  // 16-byte pieces per output row
-#pragma unroll
-        for (int k = 0; k < 16 * CPR / 64; ++k) {
-            const int e = k * 64 + lane;
-            const int row = e / CPR, col = e % CPR;
-            const float4 x = *reinterpret_cast<const float4 *>(so + row * OROW + col * 4);
-            const int qv = wq0 + qb * 16 + row;
-            if (qv < p.n_tok)
-                *reinterpret_cast<float4 *>(p.out + (((int64_t) b * p.n_tok + qv) * p.n_heads + h) * D +
-                                            col * 4) = x;
-        }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads done before the next block's writes
     }
 }
 
