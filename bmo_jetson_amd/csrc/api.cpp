@@ -9,6 +9,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -26,8 +27,9 @@ struct bmo_kv_ring {
     bmo::RingGeom g{};
     int device = 0;
     uint8_t *mem = nullptr;  // every stripe (layout in ring_layout.hpp)
-    uint8_t *stage = nullptr;  // prefill staging, grown on demand
+    uint8_t *stage = nullptr;  // prefill staging, grown on demand (guarded by stage_mu)
     int64_t stage_bytes = 0;
+    std::mutex stage_mu;
     std::mutex mu;           // guards last_error
     std::string last_error;
 };
@@ -41,10 +43,21 @@ thread_local std::string t_create_error;
 std::mutex g_registry_mu;
 std::map<const void *, bmo_kv_ring_t *> g_registry;
 
-bmo_kv_ring_t *registry_find(const void *base) {
+// Copies the geometry of the ring whose allocation starts at base, under
+// the registry lock (a concurrent bmo_kv_ring_free cannot leave a dangling
+// pointer here).  False if base is not a ring's allocation.
+bool registry_geometry(const void *base, bmo::RingGeom *g) {
     std::lock_guard<std::mutex> lk(g_registry_mu);
     auto it = g_registry.find(base);
-    return it == g_registry.end() ? nullptr : it->second;
+    if (it == g_registry.end()) return false;
+    *g = it->second->g;
+    return true;
+}
+
+// Writes one line to stderr the first time a launcher without a status
+// channel rejects its arguments (thread-safe).
+void warn_once(std::atomic<bool> &warned, const char *fn, const char *why) {
+    if (!warned.exchange(true)) std::fprintf(stderr, "[bmo_attn] %s: %s\n", fn, why);
 }
 
 constexpr float kLog2e = 1.4426950408889634f;
@@ -449,6 +462,9 @@ int bmo_kv_ring_prefill(bmo_kv_ring_t *r, int layer, int n_batch, const int *ses
         p.qscale = scale * kLog2e;
         p.sg = bmo::make_geom(1, n_batch, r->g.n_kv_heads, r->g.head_dim, n_tok);
         const int64_t need = bmo::prefill_is_direct(p) ? 0 : p.sg.total_bytes();
+        // Staged calls on one ring share its staging buffer: they must be
+        // ordered on one stream (the lock only guards the buffer's growth).
+        std::lock_guard<std::mutex> stage_lock(r->stage_mu);
         if (need > r->stage_bytes) {
             // grow-only staging; the previous one may still be read by queued work
             hipError_t e = hipStreamSynchronize((hipStream_t) stream);
@@ -599,12 +615,9 @@ int bmo_launch_gemv_q4_0_q8_1(const void *W_dev, const float *x_dev, float *y_de
     // Same arguments as src/bmo_cuda_kernels.cu:685-711 (which returns
     // nothing); rejected arguments launch nothing, are reported once on
     // stderr and return an error code.
-    static bool warned = false;
+    static std::atomic<bool> warned{false};
     auto reject = [](int code, const char *why) {
-        if (!warned) {
-            warned = true;
-            std::fprintf(stderr, "[bmo_attn] bmo_launch_gemv_q4_0_q8_1: %s\n", why);
-        }
+        warn_once(warned, "bmo_launch_gemv_q4_0_q8_1", why);
         return code;
     };
     try {
@@ -638,13 +651,8 @@ void bmo_launch_decode_attention(const float *q_dev, const float *k_dev, const f
     // Mirrors src/bmo_cuda_kernels.cu:850-884: no status is returned, so
     // rejected arguments launch nothing (as an invalid launch would) and are
     // reported on stderr once.
-    static bool warned = false;
-    auto reject = [](const char *why) {
-        if (!warned) {
-            warned = true;
-            std::fprintf(stderr, "[bmo_attn] bmo_launch_decode_attention: %s\n", why);
-        }
-    };
+    static std::atomic<bool> warned{false};
+    auto reject = [](const char *why) { warn_once(warned, "bmo_launch_decode_attention", why); };
     if (!q_dev || !k_dev || !v_dev || !k_cache_dev || !v_cache_dev || !out_dev ||
         (head_dim != 64 && head_dim != 128) || n_heads <= 0 || n_kv_heads <= 0 ||
         n_heads % n_kv_heads != 0 || n_ctx <= 0 || n_ctx > 65536 || layer < 0 ||
@@ -656,8 +664,8 @@ void bmo_launch_decode_attention(const float *q_dev, const float *k_dev, const f
     bmo::DecodeParams p{};
     // The reference cache has n_heads head slots per layer and one session.
     p.g = bmo::make_geom(layer + 1, 1, n_heads, head_dim, n_ctx);
-    if (bmo_kv_ring_t *r = registry_find(k_cache_dev)) {
-        const bmo::RingGeom &rg = r->g;
+    bmo::RingGeom rg;
+    if (registry_geometry(k_cache_dev, &rg)) {
         if (rg.head_dim != head_dim || rg.n_ctx != n_ctx || rg.n_sessions != 1 ||
             rg.n_kv_heads != n_heads || layer >= rg.n_layers)
             return reject("arguments do not match the ring's geometry");

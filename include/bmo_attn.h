@@ -203,7 +203,8 @@ BMO_ATTN_API int bmo_kv_ring_append_decode_rope(bmo_kv_ring_t *ring, int layer, 
  * n_tok <= 256 one kernel quantizes, attends and commits; otherwise the call
  * stages the chunk's Q4_0 blocks in the ring's staging buffer (n_batch *
  * n_kv_heads stripes of n_tok slots), grown on first use with a
- * synchronization of stream. */
+ * synchronization of stream; staged calls on one ring share that buffer and
+ * must therefore be ordered on one stream. */
 BMO_ATTN_API int bmo_kv_ring_prefill(bmo_kv_ring_t *ring, int layer, int n_batch,
                                      const int *session_ids, const int *pos0,
                                      int n_tok, int n_heads, const uint16_t *q,
