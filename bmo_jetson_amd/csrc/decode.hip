@@ -428,7 +428,9 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
         }
         const float pk = __builtin_amdgcn_exp2f(s - mm);  // 2^24 * weight; 0 if masked
         l += pk;
-        const float w = pk * half_of<true>(T.sc);
+        // a masked key adds exactly nothing, whatever its slot holds (a
+        // non-finite V scale outside the window must not reach the output)
+        const float w = ok ? pk * half_of<true>(T.sc) : 0.0f;
         csum += w;
         block_axpy(T.v, w, acc);
     };

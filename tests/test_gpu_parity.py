@@ -421,3 +421,39 @@ def test_b1_repeated_calls(gpu):
         if step % 2:
             p += 1
     m.assert_ring_equal(0, 0)
+
+
+@pytest.mark.parametrize("fused", [False, True])
+def test_masked_slots_with_nonfinite_scales(gpu, fused):
+    """Slots outside the window (and, fused, the current slot before the
+    write) hold blocks with infinite and NaN scales: the output depends on
+    the window only, so it stays finite and matches the oracle."""
+    n_kv, d, n_ctx = 4, 128, 64
+    m = Mirror(gpu, 1, 1, n_kv, d, n_ctx)
+    pos = 20  # window 21 (fused: 20 ring keys + the new one); slots 21.. are outside
+    m.fill_range(0, 0, 0, pos, seed=77)
+    nblk = d // 32
+    bad = np.zeros((n_ctx - pos, n_kv, nblk), dtype=oracle.BLOCK_DTYPE)
+    bad["d"] = np.where(np.arange(n_ctx - pos)[:, None, None] % 2 == 0, 0x7C00, 0x7E00)  # inf / NaN
+    bad["qs"] = 0x3C
+    for which in (0, 1):
+        m.ring.import_q4_0(0, 0, which, pos, bad.view(np.uint8))
+    gpu.cuda.synchronize()
+    n_heads = 8
+    q = oracle.normal(78, n_heads * d)
+    out = gpu.full((n_heads * d,), float("nan"), dtype=gpu.float32, device="cuda")
+    posd = _i32(gpu, [pos])
+    if fused:
+        k = oracle.normal(79, n_kv * d)
+        v = oracle.normal(80, n_kv * d)
+        m.ring.append_decode(0, posd, m.dev(q), m.dev(k), m.dev(v), out, n_heads, stream=m.stream)
+        m.oracle_append(0, 0, pos, k, v)
+    else:
+        m.oracle_append(0, 0, pos, oracle.normal(81, n_kv * d), oracle.normal(82, n_kv * d))
+        kk = oracle.normal(81, n_kv * d)
+        vv = oracle.normal(82, n_kv * d)
+        m.ring.append(0, posd, m.dev(kk), m.dev(vv), stream=m.stream)
+        m.ring.decode(0, posd, m.dev(q), out, n_heads, stream=m.stream)
+    gpu.cuda.synchronize()
+    got = out.cpu().numpy().reshape(n_heads, d)
+    check_close(got, m.oracle_decode(0, 0, pos, q, n_heads), f"non-finite outside the window, fused={fused}")
