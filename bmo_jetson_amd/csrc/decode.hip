@@ -303,10 +303,16 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     const int cur = pos % g.n_ctx;
     uint8_t *stripe = p.base + g.stripe_offset(p.layer, sid, kvh);
 
-    // Contiguous group run of this wave.
+    // Contiguous group run of this wave.  Fused with several waves per
+    // unit, wave 0 quantizes and attends to the current token and the other
+    // waves split the window, so the new token's work is off the window's
+    // critical path.
     const int n_grp = (window + G - 1) / G;
-    const int g0 = wave * n_grp / NW;
-    const int n_it = (wave + 1) * n_grp / NW - g0;
+    constexpr bool kSplitNew = FUSED && NW > 1;
+    constexpr int NWW = kSplitNew ? NW - 1 : NW;  // waves that stream the window
+    const int ww = kSplitNew ? wave - 1 : wave;
+    const int g0 = ww < 0 ? 0 : ww * n_grp / NWW;
+    const int n_it = ww < 0 ? 0 : (ww + 1) * n_grp / NWW - g0;
 
     struct Grp {
         uint4 k, v;
