@@ -93,19 +93,29 @@ __host__ __device__ constexpr int col_elem(int s) {
     return (s & ~31) + 4 * ((s & 31) >> 3) + perm_elem(s & 7);
 }
 
-// Dequantizes code dword w (plain codes, bytes 4c..4c+3 of a block) with
-// fp16 scale bits d16 into 8 fp16 values in perm_elem order:
-// (code - 8) * d, the subtraction exact, the product rounded to nearest.
-__device__ __forceinline__ half8_t dequant_dword(uint32_t w, uint32_t d16) {
-    const half2_t off = {(_Float16) -1032.0f, (_Float16) -1032.0f};
+// xor constants of dequant_dword: stored K nibbles are code ^ 8, V nibbles
+// plain codes.
+constexpr uint32_t kXorLoK = 0x64086408u, kXorHiK = 0x54805480u;
+constexpr uint32_t kXorLoV = 0x64006400u, kXorHiV = 0x54005400u;
+
+// Dequantizes code dword w (bytes 4c..4c+3 of a block) with fp16 scale bits
+// d16 (low half) into 8 fp16 values in perm_elem order: (code - 8) * d, the
+// subtraction exact, the product rounded to nearest.  A low nibble n under
+// the fp16 pattern 0x6400 reads 1024 + n; a high nibble, left in place
+// (n << 4) under 0x5400, reads 64 + n, so no shift per nibble is needed.
+// xlo/xhi are those patterns, K's with the stored bit 3 flipped back (the xor
+// touches only nibble bits and the pattern's own, disjoint bits).
+__device__ __forceinline__ half8_t dequant_dword(uint32_t w, uint32_t d16, uint32_t xlo, uint32_t xhi) {
+    const half2_t off_lo = {(_Float16) -1032.0f, (_Float16) -1032.0f};
+    const half2_t off_hi = {(_Float16) -72.0f, (_Float16) -72.0f};
     const _Float16 d = __builtin_bit_cast(_Float16, (uint16_t) d16);
     const half2_t dd = {d, d};
+    const uint32_t y = w >> 8;
     half2_t r[4];
-    const uint32_t src[4] = {w & 0x000F000Fu, (w >> 8) & 0x000F000Fu, (w >> 4) & 0x000F000Fu,
-                             (w >> 12) & 0x000F000Fu};
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-        r[i] = (__builtin_bit_cast(half2_t, src[i] | 0x64006400u) + off) * dd;
+    r[0] = (__builtin_bit_cast(half2_t, (w & 0x000F000Fu) ^ xlo) + off_lo) * dd;
+    r[1] = (__builtin_bit_cast(half2_t, (y & 0x000F000Fu) ^ xlo) + off_lo) * dd;
+    r[2] = (__builtin_bit_cast(half2_t, (w & 0x00F000F0u) ^ xhi) + off_hi) * dd;
+    r[3] = (__builtin_bit_cast(half2_t, (y & 0x00F000F0u) ^ xhi) + off_hi) * dd;
     // r[0] = (e0, e2), r[1] = (e1, e3), r[2] = (e16, e18), r[3] = (e17, e19)
     half8_t o;
     o[0] = r[0].x;
@@ -189,7 +199,7 @@ __global__ __launch_bounds__(256) void commit_kernel(PrefillParams p) {
 // reads the chunk's keys from there, and writes the chunk's blocks into the
 // ring after its last tile, when no wave reads the old slots any more; no
 // stage or commit kernel runs.
-template <int D, int QW, int QB, bool DIRECT>
+template <int D, int QW, int QB, bool DIRECT, bool ALIGNED>
 __global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams p) {
     constexpr int NBLK = D / kQK;
     // LDS rows (fp16): K rows padded to 68 dwords so that the 16 lanes of an
@@ -248,108 +258,147 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams 
     const int p_first = pos0 + i0;
     const int p_last = pos0 + i0 + nq - 1;
     const int k_lo = max(0, p_first - n_ctx + 1);
-    const int n_tiles = (p_last - k_lo) / kTK + 1;
+    // Tiles: the ring's keys k_lo .. pos0 - 1 in tiles aligned to 32
+    // positions (tiles 0 .. n_rt - 1), then the chunk's keys in tiles
+    // aligned to pos0, so that no tile mixes ring and chunk keys.  A key of a
+    // tile outside its source's live range (ring [k_lo, pos0), chunk
+    // [pos0, p_last]) is dequantized with scale 0 and masked.
+    const int r_start = k_lo & ~(kTK - 1);
+    const int n_rt = k_lo < pos0 ? (pos0 - 1 - r_start) / kTK + 1 : 0;
+    const int c_start = pos0 + ((max(k_lo, pos0) - pos0) & ~(kTK - 1));
+    const int n_tiles = n_rt + (p_last - c_start) / kTK + 1;
+    auto tile_t0 = [&](int T) { return T < n_rt ? r_start + T * kTK : c_start + (T - n_rt) * kTK; };
     const uint8_t *ring = p.base + p.g.stripe_offset(p.layer, sid, kvh);
     const uint8_t *stage = p.stage + p.sg.stripe_offset(0, b, kvh);
     const uint32_t ring_gs = (uint32_t) p.g.group_stride;
     const uint32_t stage_gs = (uint32_t) p.sg.group_stride;
 
     // This thread's items: item j is (K/V, key, block, 8-byte half) =
-    // (which, key, bb, hf) of every tile.  The fetch walks the tiles in order
-    // and keeps, per item, the position t of its key in the tile being
-    // fetched and that position's ring slot t % n_ctx.
-    int it_key[IPT];
-    uint32_t it_code[IPT], it_scale[IPT];  // byte offsets inside a group
-    int ft[IPT], fslot[IPT];
-    const int slot_step = kTK % n_ctx;
+    // (which, key, bb, hf) of every tile.  A wave's 64 items share `which`
+    // and the key's slot group key / G (static_asserts below), so those are
+    // scalars and a tile's loads use a scalar group address plus these
+    // per-item offsets inside the group.
+    static_assert((2 * kTK * NBLK) % 64 == 0, "a wave's items share K/V");
+    static_assert(G % (32 / NBLK) == 0, "a wave's items share a slot group");
+    int it_key[IPT], it_grp[IPT];
+    bool it_v[IPT];
+    uint32_t it_code[IPT], it_scale[IPT], it_lds[IPT], it_slds[IPT];
 #pragma unroll
     for (int j = 0; j < IPT; ++j) {
         const int it = min((int) threadIdx.x + j * NTHR, ITEMS - 1);
         const int hf = it & 1;
         const int bb = (it >> 1) % NBLK;
         const int key = (it >> 1) / NBLK % kTK;
-        const int which = it / (2 * kTK * NBLK);
+        const int which = __builtin_amdgcn_readfirstlane(it / (2 * kTK * NBLK));
         it_key[j] = key;
-        it_code[j] = bb * 16 + which * kVCodeOff + 8 * hf;
-        it_scale[j] = kScaleOff + bb * 4;  // the (K, V) scale dword
-        ft[j] = k_lo + key;
-        fslot[j] = ft[j] % n_ctx;
+        it_grp[j] = __builtin_amdgcn_readfirstlane(key / G);
+        it_v[j] = which != 0;
+        it_code[j] = (uint32_t) ((key % G) * (D / 2) + bb * 16 + which * kVCodeOff + 8 * hf);
+        it_scale[j] = (uint32_t) (kScaleOff + ((key % G) * NBLK + bb) * 4);
+        it_lds[j] = (uint32_t) (((which * QT + key) * NBLK + bb) * 16 + 8 * hf);
+        it_slds[j] = (uint32_t) ((key * NBLK + bb) * 4);
     }
 
     // Raw tile bytes, fetched PF tiles ahead: this thread's items.  Every
-    // fetch issues its loads (a key past the chunk reads a ring slot and is
-    // dequantized with scale 0), so the number of loads in flight is the same
-    // on every path and the compiler's waits stay exact; the liveness flag is
-    // applied at dequantization, not at the load.
+    // fetch issues its loads (tiles whose keys come from elsewhere -- DIRECT
+    // chunk tiles, padding tiles past the end -- read the ring stripe's first
+    // slots, which stay cached), so the number of loads in flight is the same
+    // on every path and the compiler's waits stay exact.
     constexpr int PF = 7;
     static_assert((PF + 1) % NBUF == 0, "the unrolled slot must determine the LDS buffer");
     uint2 raw[PF + 1][IPT];
     uint32_t rawd[PF + 1][IPT];
-    bool rawl[PF + 1][IPT];
-    auto fetch = [&](uint2 (&rw)[IPT], uint32_t (&rd)[IPT], bool (&rl)[IPT]) {
+    int f_tile = 0;                  // next tile to fetch
+    int f_slot = r_start % n_ctx;    // its ring slot, while it is a ring tile
+    auto fetch = [&](uint2 (&rw)[IPT], uint32_t (&rd)[IPT]) {
+        const int T = f_tile++;
+        const bool ring_t = T < n_rt;
+        const bool staged_t = !DIRECT && !ring_t && T < n_tiles;
+        // Scalar: the slot group of the tile's first key (ALIGNED: a ring
+        // tile's slots t0 % n_ctx .. +31 never wrap) and the last group the
+        // tile may address; keys past the staged chunk clamp to its last
+        // group, and a tile with no keys to load reads group 0 only, so
+        // every address stays inside the stripe.
+        const int g_first = staged_t ? (tile_t0(T) - pos0) / G : ring_t ? f_slot / G : 0;
+        const int g_last = staged_t ? p.sg.n_groups - 1 : ring_t ? p.g.n_groups - 1 : 0;
+        const uint8_t *gsrc = staged_t ? stage : ring;
+        const uint32_t gs = staged_t ? stage_gs : ring_gs;
+        const int slot0 = f_slot;
+        if (ring_t) {
+            f_slot += kTK;
+            if (f_slot >= n_ctx) f_slot -= n_ctx;
+            if (!ALIGNED && f_slot >= n_ctx) f_slot %= n_ctx;
+        }
 #pragma unroll
         for (int j = 0; j < IPT; ++j) {
-            const int t = ft[j];
-            // Older keys come from the ring, chunk keys from the staging
-            // stripe (slot t - pos0), or in DIRECT mode from LDS at deposit.
-            // Loads that carry no key (DIRECT chunk keys, keys past the
-            // chunk) read the ring stripe's slot 0, which stays cached: the
-            // load count is uniform and no HBM bytes are spent on them.
-            const bool past = t > p_last;
-            const bool staged = !DIRECT && t >= pos0 && !past;
-            const bool dummy = past || (DIRECT && t >= pos0);
-            const int slot = staged ? t - pos0 : dummy ? 0 : fslot[j];
-            const uint8_t *gp = (staged ? stage : ring) +
-                                (uint64_t) (uint32_t) (slot / G) * (staged ? stage_gs : ring_gs);
-            const uint32_t row = (uint32_t) (slot % G);
-            rw[j] = *reinterpret_cast<const uint2 *>(gp + row * (D / 2) + it_code[j]);
+            const uint8_t *gp = gsrc + (uint64_t) (uint32_t) min(g_first + it_grp[j], g_last) * gs;
+            uint32_t co = it_code[j], so = it_scale[j];
+            if constexpr (!ALIGNED) {
+                // the ring's slots wrap inside a tile: per-key slot
+                if (ring_t) {
+                    const uint32_t slot = (uint32_t) (slot0 + it_key[j]) % (uint32_t) n_ctx;
+                    const uint32_t row = slot % G;
+                    const uint32_t in_row = it_code[j] - (uint32_t) (it_key[j] % G) * (D / 2);
+                    gp = ring + (uint64_t) (slot / G) * ring_gs;
+                    co = row * (D / 2) + in_row;
+                    so = it_scale[j] + (row - (uint32_t) (it_key[j] % G)) * (NBLK * 4);
+                }
+            }
+            rw[j] = *reinterpret_cast<const uint2 *>(gp + co);
             // the whole scale dword: a 16-bit load would be zero-extended
             // into a copy that hipcc places at the loop's back edge, waiting
             // for the load there
-            rd[j] = *reinterpret_cast<const uint32_t *>(gp + row * (NBLK * 4) + it_scale[j]);
-            rl[j] = t <= p_last && (int) threadIdx.x + j * NTHR < ITEMS;
-            ft[j] = t + kTK;
-            const int ns = fslot[j] + slot_step;
-            fslot[j] = ns >= n_ctx ? ns - n_ctx : ns;
+            rd[j] = *reinterpret_cast<const uint32_t *>(gp + so);
         }
     };
-    // Dequantizes fetched items into LDS buffer `buf`: K and V row-major,
-    // the values of code dword cd at slots 8cd..8cd+7 of the block (the order
-    // the query operand uses; col_elem maps a column back to its element).
-    auto deposit = [&](int buf, int t0, const uint2 (&rw)[IPT], const uint32_t (&rd)[IPT],
-                       const bool (&rl)[IPT]) {
+    // Dequantizes fetched items of tile T into LDS buffer `buf`: K and V
+    // row-major, the values of code dword cd at slots 8cd..8cd+7 of the block
+    // (the order the query operand uses; col_elem maps a column back to its
+    // element).
+    auto deposit = [&](int buf, int T, const uint2 (&rw)[IPT], const uint32_t (&rd)[IPT]) {
+        const bool ring_t = T < n_rt;
+        const int t0 = tile_t0(T);
+        const int lo = ring_t ? k_lo : pos0;
+        const uint32_t span = (uint32_t) ((ring_t ? pos0 - 1 : p_last) - lo);
+        // DIRECT chunk tiles: the chunk's blocks in LDS (clamped for padding
+        // tiles, whose keys are all dead)
+        const uint32_t coff = (uint32_t) min(max(t0 - pos0, 0), QT - kTK) * (NBLK * 16);
 #pragma unroll
         for (int j = 0; j < IPT; ++j) {
             const int it = threadIdx.x + j * NTHR;
             if (it < ITEMS) {
-                const int hf = it & 1;
-                const int bb = (it >> 1) % NBLK;
                 const int key = it_key[j];
-                const int which = it / (2 * kTK * NBLK);
+                const bool live = (uint32_t) (t0 + key - lo) <= span;
                 uint2 w = rw[j];
                 uint32_t sd = rd[j];
                 if constexpr (DIRECT) {
-                    // chunk token i of this key, if any: its blocks are in LDS
-                    const int i = t0 + key - pos0;
-                    const int ic = min(max(i, 0), QT - 1);
-                    const uint2 cw = reinterpret_cast<const uint2 *>(&sCc[(which * QT + ic) * NBLK + bb])[hf];
-                    const uint32_t cs = sCs[ic * NBLK + bb];
-                    w = i >= 0 ? cw : w;
-                    sd = i >= 0 ? cs : sd;
+                    const uint8_t *cp = reinterpret_cast<const uint8_t *>(sCc) + it_lds[j] + coff;
+                    const uint2 cw = *reinterpret_cast<const uint2 *>(cp);
+                    const uint32_t cs = *reinterpret_cast<const uint32_t *>(
+                        reinterpret_cast<const uint8_t *>(sCs) + it_slds[j] + coff / 4);
+                    w = ring_t ? w : cw;
+                    sd = ring_t ? sd : cs;
                 }
-                const uint32_t flip = which == 0 ? 0x88888888u : 0u;  // K codes are stored as code ^ 8
-                const uint32_t dw = which == 0 ? sd & 0xFFFFu : sd >> 16;
-                const uint32_t d16 = rl[j] ? dw : 0u;  // scale 0 past the chunk
-                const half8_t v0 = dequant_dword(w.x ^ flip, d16);
-                const half8_t v1 = dequant_dword(w.y ^ flip, d16);
-                _Float16 *dst = which == 0 ? &sK[buf][key * KROW + bb * kQK + 16 * hf]
-                                           : &sV[buf][key * VROW + bb * kQK + 16 * hf];
+                const uint32_t dw = it_v[j] ? sd >> 16 : sd;
+                const uint32_t d16 = live ? dw : 0u;
+                const uint32_t xlo = it_v[j] ? kXorLoV : kXorLoK;
+                const uint32_t xhi = it_v[j] ? kXorHiV : kXorHiK;
+                const half8_t v0 = dequant_dword(w.x, d16, xlo, xhi);
+                const half8_t v1 = dequant_dword(w.y, d16, xlo, xhi);
+                const int bb = (it >> 1) % NBLK;
+                const int hf = it & 1;
+                _Float16 *dst = it_v[j] ? &sV[buf][key * VROW + bb * kQK + 16 * hf]
+                                        : &sK[buf][key * KROW + bb * kQK + 16 * hf];
                 *reinterpret_cast<half8_t *>(dst) = v0;
                 *reinterpret_cast<half8_t *>(dst + 8) = v1;
             }
         }
     };
 
+
+    // Loads, in the order they are waited for (loads return in order): the
+    // query rows, the first PF tiles, then (DIRECT) the chunk's bf16 K/V; the
+    // query conversion runs while the later ones are in flight.
     // Query operands (B of S^T = K Q^T): for query block qb lane l holds
     // query n = l % 16 of that block, block b's values at elements
     // 4c + perm_elem(r), c = l / 16.  Rows past the chunk read row 0 and are
@@ -357,26 +406,60 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams 
     const int n = lane & 15;
     const int c = lane >> 4;
     const int wq0 = i0 + wave * QWV;  // first query of this wave
-    half8_t qop[QB][NBLK];
+    uint2 qlo[QB][NBLK], qhi[QB][NBLK];
     int mrel[QB];  // this lane's query position minus 4c (mask arithmetic)
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
         const int qi = wq0 + qb * 16 + n;
-        const bool q_ok = qi < p.n_tok;
         mrel[qb] = pos0 + qi - 4 * c;
-        const uint16_t *qrow = p.q + (((int64_t) b * p.n_tok + (q_ok ? qi : 0)) * p.n_heads + h) * D;
-        uint2 lo[NBLK], hi[NBLK];
+        const uint16_t *qrow = p.q + (((int64_t) b * p.n_tok + (qi < p.n_tok ? qi : 0)) * p.n_heads + h) * D;
 #pragma unroll
         for (int bb = 0; bb < NBLK; ++bb) {
-            lo[bb] = *reinterpret_cast<const uint2 *>(qrow + bb * kQK + 4 * c);
-            hi[bb] = *reinterpret_cast<const uint2 *>(qrow + bb * kQK + 4 * c + 16);
+            qlo[qb][bb] = *reinterpret_cast<const uint2 *>(qrow + bb * kQK + 4 * c);
+            qhi[qb][bb] = *reinterpret_cast<const uint2 *>(qrow + bb * kQK + 4 * c + 16);
         }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // The trip count is padded to a multiple of PF + 1 tiles (an empty tile
+    // past the chunk is zeros and skipped by every wave), so the unrolled
+    // body has no per-tile condition around its loads.  The scheduling
+    // barriers keep hipcc from hoisting later loads above earlier ones, so
+    // that each wait covers the oldest loads only.
+#pragma unroll
+    for (int j = 0; j < PF; ++j) {
+        fetch(raw[j], rawd[j]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // DIRECT: this thread's blocks of the chunk's K and V (bf16), all in
+    // flight at once
+    constexpr int NQ = DIRECT ? (2 * QT * NBLK + NTHR - 1) / NTHR : 1;
+    uint4 braw[NQ][4];
+    if constexpr (DIRECT) {
+        const int nblocks = 2 * p.n_tok * NBLK;
+#pragma unroll
+        for (int k = 0; k < NQ; ++k) {
+            const int e = min((int) threadIdx.x + k * NTHR, nblocks - 1);
+            const int bb = e % NBLK;
+            const int i = (e / NBLK) % p.n_tok;
+            const int which = e / (NBLK * p.n_tok);
+            const uint4 *src = reinterpret_cast<const uint4 *>(
+                (which == 0 ? p.k : p.v) + (((int64_t) b * p.n_tok + i) * p.n_kv + kvh) * D + bb * kQK);
+#pragma unroll
+            for (int cq = 0; cq < 4; ++cq) braw[k][cq] = src[cq];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    half8_t qop[QB][NBLK];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+        const bool q_ok = wq0 + qb * 16 + n < p.n_tok;
 #pragma unroll
         for (int bb = 0; bb < NBLK; ++bb) {
             // elements 4c + {0,1,2,3} in lo, 4c + 16 + {0,1,2,3} in hi; the
             // operand order is perm_elem: 0, 2, 1, 3, 16, 18, 17, 19
-            const uint32_t e[8] = {lo[bb].x & 0xFFFFu, lo[bb].y & 0xFFFFu, lo[bb].x >> 16, lo[bb].y >> 16,
-                                   hi[bb].x & 0xFFFFu, hi[bb].y & 0xFFFFu, hi[bb].x >> 16, hi[bb].y >> 16};
+            const uint2 lo = qlo[qb][bb], hi = qhi[qb][bb];
+            const uint32_t e[8] = {lo.x & 0xFFFFu, lo.y & 0xFFFFu, lo.x >> 16, lo.y >> 16,
+                                   hi.x & 0xFFFFu, hi.y & 0xFFFFu, hi.x >> 16, hi.y >> 16};
 #pragma unroll
             for (int r = 0; r < 8; ++r)
                 qop[qb][bb][r] = (_Float16) (q_ok ? bf16_to_f32(e[r]) * p.qscale : 0.0f);
@@ -404,7 +487,9 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams 
     const half8_t ones = {(_Float16) 1.0f, (_Float16) 1.0f, (_Float16) 1.0f, (_Float16) 1.0f,
                           (_Float16) 1.0f, (_Float16) 1.0f, (_Float16) 1.0f, (_Float16) 1.0f};
 
-    auto compute = [&](int buf, int t0) {
+    auto compute = [&](int buf, int T) {
+        const bool ring_t = T < n_rt;
+        const int t0 = tile_t0(T);
         if (wq0 >= p.n_tok || t0 > w_hi || t0 + kTK - 1 < w_lo) return;  // nothing to see
         // S^T for keys 0..15 and 16..31 of the tile: lane l gets keys
         // 4c + v (and 16 + 4c + v) of query n of each query block.
@@ -425,19 +510,23 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams 
         // Mask (causal + window) unless every key of the tile is visible to
         // every query of the wave.  Query rows past the chunk are left
         // unmasked: their scores are finite and their outputs never stored.
-        const bool whole = t0 + kTK - 1 <= pos0 + wq0 && t0 > w_hi - n_ctx;
+        // A ring tile's keys must also precede pos0 (its last tile may reach
+        // into the chunk's positions, which the chunk tiles supply).
+        const bool whole = t0 + kTK - 1 <= (ring_t ? pos0 - 1 : pos0 + wq0) && t0 > w_hi - n_ctx;
         if (!whole) {
 #pragma unroll
             for (int qb = 0; qb < QB; ++qb) {
                 // key t0 + 16 sub + 4c + v is visible to query position P iff
-                // P - n_ctx < t <= P, i.e. 16 sub + v in (rel - n_ctx, rel]
+                // P - n_ctx < t <= P (and t < pos0 in a ring tile; every
+                // P >= pos0), i.e. 16 sub + v in (rel - n_ctx, rel_hi]
                 const int rel = mrel[qb] - t0;
+                const int rel_hi = ring_t ? pos0 - 1 - 4 * c - t0 : rel;
 #pragma unroll
                 for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
                     for (int v = 0; v < 4; ++v) {
                         const int kk = sub * 16 + v;
-                        const bool ok = kk <= rel && kk > rel - n_ctx;
+                        const bool ok = kk <= rel_hi && kk > rel - n_ctx;
                         s[qb][sub][v] = ok ? s[qb][sub][v] : -INFINITY;
                     }
             }
@@ -489,34 +578,10 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams 
         }
     };
 
-    // The trip count is padded to a multiple of PF + 1 tiles (an empty tile
-    // past the chunk is zeros and skipped by every wave), so the unrolled
-    // body has no per-tile condition around its loads.
-    // The prologue issues its loads in the loop's order (the scheduling
-    // barriers keep hipcc from hoisting later tiles' loads), so that the
-    // loop header waits for the oldest tile only.
-#pragma unroll
-    for (int j = 0; j < PF; ++j) {
-        fetch(raw[j], rawd[j], rawl[j]);
-        __builtin_amdgcn_sched_barrier(0);
-    }
-    if constexpr (DIRECT) {
-        // the chunk's K and V blocks (bf16 -> Q4_0, the append quantizer)
-        // into LDS in ring format; the barrier publishes them
-        constexpr int NQ = (2 * QT * NBLK + NTHR - 1) / NTHR;
+    // DIRECT: the chunk's K and V blocks (bf16 -> Q4_0, the append
+    // quantizer) into LDS in ring format; the barrier publishes them
+    auto quantize_chunk = [&]() {
         const int nblocks = 2 * p.n_tok * NBLK;
-        uint4 braw[NQ][4];  // this thread's blocks as loaded (bf16), all loads in flight at once
-#pragma unroll
-        for (int k = 0; k < NQ; ++k) {
-            const int e = min((int) threadIdx.x + k * NTHR, nblocks - 1);
-            const int bb = e % NBLK;
-            const int i = (e / NBLK) % p.n_tok;
-            const int which = e / (NBLK * p.n_tok);
-            const uint4 *src = reinterpret_cast<const uint4 *>(
-                (which == 0 ? p.k : p.v) + (((int64_t) b * p.n_tok + i) * p.n_kv + kvh) * D + bb * kQK);
-#pragma unroll
-            for (int cq = 0; cq < 4; ++cq) braw[k][cq] = src[cq];
-        }
 #pragma unroll
         for (int k = 0; k < NQ; ++k) {
             const int e = min((int) threadIdx.x + k * NTHR, nblocks - 1);
@@ -544,25 +609,26 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams 
             }
         }
         lds_barrier();
-    }
+    };
     // Tile T lives in raw slot T % (PF + 1) and LDS buffer T % NBUF; its
     // loads are issued PF tiles ahead, into the slot of tile T - 1.  Buffer
     // safety: the barrier of a tile pair follows every wave's multiplication
     // of the pair before, so writing a buffer NBUF tiles later is safe.
+    if constexpr (DIRECT) quantize_chunk();
     for (int base = 0; base < n_tiles; base += PF + 1) {
 #pragma unroll
         for (int u = 0; u <= PF; u += TPB) {
 #pragma unroll
             for (int k = 0; k < TPB; ++k)
-                deposit((u + k) % NBUF, k_lo + (base + u + k) * kTK, raw[u + k], rawd[u + k], rawl[u + k]);
+                deposit((u + k) % NBUF, base + u + k, raw[u + k], rawd[u + k]);
             lds_barrier();  // these TPB buffers are complete
 #pragma unroll
             for (int k = 0; k < TPB; ++k) {
                 const int nxt = (u + k + PF) % (PF + 1);
-                fetch(raw[nxt], rawd[nxt], rawl[nxt]);
+                fetch(raw[nxt], rawd[nxt]);
             }
 #pragma unroll
-            for (int k = 0; k < TPB; ++k) compute((u + k) % NBUF, k_lo + (base + u + k) * kTK);
+            for (int k = 0; k < TPB; ++k) compute((u + k) % NBUF, base + u + k);
         }
     }
 
@@ -613,7 +679,11 @@ int prefill_waves(const PrefillParams &p) {
 
 template <int D, int QW, bool DIRECT>
 void launch_attention(const PrefillParams &p, dim3 grid, hipStream_t stream) {
-    hipLaunchKernelGGL((prefill_kernel<D, QW, 2, DIRECT>), grid, dim3(64 * QW), 0, stream, p);
+    // ring tiles 32 slots wide never wrap when n_ctx is a multiple of 32
+    if (p.g.n_ctx % kTK == 0)
+        hipLaunchKernelGGL((prefill_kernel<D, QW, 2, DIRECT, true>), grid, dim3(64 * QW), 0, stream, p);
+    else
+        hipLaunchKernelGGL((prefill_kernel<D, QW, 2, DIRECT, false>), grid, dim3(64 * QW), 0, stream, p);
 }
 
 template <int D>

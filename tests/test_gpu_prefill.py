@@ -64,6 +64,19 @@ def test_prefill_parity(gpu, pos0, n_tok):
     _run(gpu, m, layer, [(0, pos0)], n_tok, n_heads, seed=100 + n_tok)
 
 
+@pytest.mark.parametrize("n_ctx,pos0,n_tok,n_heads,n_kv", [
+    (40, 90, 30, 4, 4),     # 32-key ring tiles wrap inside the ring (one workgroup per stripe)
+    (8, 5, 8, 4, 4),        # an 8-slot ring (the depformer's), chunk as long as the ring
+    (72, 100, 60, 8, 2),    # staged chunk (4 query heads per kv head)
+    (100, 1000, 100, 4, 4),
+    (96, 70, 9, 4, 4),      # ring tiles aligned, last one partial
+])
+def test_prefill_ring_sizes(gpu, n_ctx, pos0, n_tok, n_heads, n_kv):
+    m = Mirror(gpu, 1, 1, n_kv, 128, n_ctx)
+    m.fill_range(0, 0, 0, pos0, seed=300 + n_ctx)
+    _run(gpu, m, 0, [(0, pos0)], n_tok, n_heads, seed=310 + n_ctx)
+
+
 def test_prefill_gqa_and_head_dim_64(gpu):
     m = Mirror(gpu, 1, 1, 2, 128, 96)
     m.fill_range(0, 0, 0, 150, seed=31)
