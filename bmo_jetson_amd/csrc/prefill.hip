@@ -69,6 +69,12 @@ __device__ __forceinline__ half4_t lds_read_tr16(const _Float16 *p) {
     return __builtin_bit_cast(half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_fp16x4 *) p));
 }
 
+// The value of v in lane (l & ~3) + (CTRL >> 2(l & 3)) & 3 (DPP quad_perm).
+template <int CTRL>
+__device__ __forceinline__ float quad_perm(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
 // Maximum without operand canonicalization (v_maximum3_f32): scores are
 // never NaN, and fmaxf's quieting of signalling NaNs costs an instruction per
 // operand.
@@ -92,6 +98,19 @@ __host__ __device__ constexpr int perm_elem(int r) {
 __host__ __device__ constexpr int col_elem(int s) {
     return (s & ~31) + 4 * ((s & 31) >> 3) + perm_elem(s & 7);
 }
+
+// The output store's float4 layout: lane 4qd + j of a 16-lane group holds
+// column slot 16t + 4qd + j, element base(qd, t) + {0, 2, 1, 3}[j].
+__host__ __device__ constexpr bool store_layout_matches() {
+    for (int t = 0; t < 8; ++t)
+        for (int n = 0; n < 16; ++n) {
+            const int qd = n >> 2, j = n & 3;
+            const int base = 32 * (t >> 1) + 8 * (t & 1) + 4 * (qd >> 1) + 16 * (qd & 1);
+            if (col_elem(16 * t + n) != base + (j == 1 ? 2 : j == 2 ? 1 : j)) return false;
+        }
+    return true;
+}
+static_assert(store_layout_matches(), "output float4 layout");
 
 // xor constants of dequant_dword: stored K nibbles are code ^ 8, V nibbles
 // plain codes.
@@ -650,18 +669,43 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams 
         }
     }
 
-    // Every acc row (query 4c + v) divides by its weight sum.
+    // Every acc row (query 4c + v) divides by its weight sum.  Lane 4qd + j
+    // (of the 16 sharing c) holds, for column tile t, element
+    // 32(t / 2) + 8(t % 2) + 4(qd / 2) + 16(qd % 2) + {0, 2, 1, 3}[j] of the
+    // row (col_elem), i.e. the 4 lanes of a quad hold one float4 of the row
+    // per t.  A 4x4 transpose inside the quad (DPP lane ^ 1, lane ^ 2) over
+    // t = 4g .. 4g + 3 gives lane j the whole float4 of t = 4g + j, so each
+    // lane stores 16-byte pieces and a store instruction covers 256
+    // contiguous bytes of each of 4 rows.
+    const int jq = lane & 3;
+    const int qd = (lane >> 2) & 3;
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             const float lv = accl[qb][v];
             const int qv = wq0 + qb * 16 + 4 * c + v;
-            if (qv < p.n_tok) {
-                float *orow = p.out + (((int64_t) b * p.n_tok + qv) * p.n_heads + h) * D;
-                const float inv = lv > 0.0f ? 1.0f / lv : 0.0f;
+            const float inv = lv > 0.0f ? 1.0f / lv : 0.0f;
+            float *orow = p.out + (((int64_t) b * p.n_tok + min(qv, p.n_tok - 1)) * p.n_heads + h) * D;
 #pragma unroll
-                for (int t = 0; t < NT; ++t) orow[col_elem(t * 16 + n)] = acc[qb][t][v] * inv;
+            for (int g = 0; g < NT / 4; ++g) {
+                const float a0 = acc[qb][4 * g][v] * inv, a1 = acc[qb][4 * g + 1][v] * inv;
+                const float a2 = acc[qb][4 * g + 2][v] * inv, a3 = acc[qb][4 * g + 3][v] * inv;
+                // every lane reads its partner before the selects: a DPP
+                // read from a lane the branch disabled returns nothing
+                const bool odd = jq & 1, up = jq & 2;
+                const float x0 = quad_perm<0xB1>(a0), x1 = quad_perm<0xB1>(a1);
+                const float x2 = quad_perm<0xB1>(a2), x3 = quad_perm<0xB1>(a3);
+                const float b0 = odd ? x1 : a0, b1 = odd ? a1 : x0;
+                const float b2 = odd ? x3 : a2, b3 = odd ? a3 : x2;
+                const float y0 = quad_perm<0x4E>(b0), y1 = quad_perm<0x4E>(b1);
+                const float y2 = quad_perm<0x4E>(b2), y3 = quad_perm<0x4E>(b3);
+                const float c0 = up ? y2 : b0, c1 = up ? y3 : b1;
+                const float c2 = up ? b2 : y0, c3 = up ? b3 : y1;
+                // c_k is element base + {0, 2, 1, 3}[k] of tile t = 4g + jq
+                const int t = 4 * g + jq;
+                const int base = 32 * (t >> 1) + 8 * (t & 1) + 4 * (qd >> 1) + 16 * (qd & 1);
+                if (qv < p.n_tok) *reinterpret_cast<float4 *>(orow + base) = make_float4(c0, c2, c1, c3);
             }
         }
     }
