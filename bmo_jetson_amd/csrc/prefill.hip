@@ -36,7 +36,6 @@
 // as the reference's F16 cache requires.
 #include <limits.h>
 #include <math.h>
-#include <stdlib.h>
 
 #include "kernels.hpp"
 #include "q4_0_device.hpp"
@@ -713,36 +712,30 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams 
 
 namespace {
 
-// 32 queries per wave; 8 waves (256 queries, one workgroup per chunk of a
-// head) or 4.  BMO_PREFILL_WAVES = 4 | 8 overrides (tuning).
-int prefill_waves(const PrefillParams &p) {
-    int qw = p.n_tok > 128 ? 8 : 4;
-    if (const char *e = std::getenv("BMO_PREFILL_WAVES")) qw = std::atoi(e) == 4 ? 4 : 8;
-    return qw;
-}
+// 8 waves x 32 queries: one workgroup per 256 queries of a head.  Smaller
+// workgroups for short chunks (4 waves below 129 tokens) were measured slower
+// whenever the ring holds history (64.6 vs 58.9 us at 16 tokens, 79.8 vs
+// 71.5 us at 128, cfg5 shape): the window's tiles dominate, and 8 waves
+// share their dequantization.
+constexpr int kQW = 8;
 
-template <int D, int QW, bool DIRECT>
+template <int D, bool DIRECT>
 void launch_attention(const PrefillParams &p, dim3 grid, hipStream_t stream) {
     // ring tiles 32 slots wide never wrap when n_ctx is a multiple of 32
     if (p.g.n_ctx % kTK == 0)
-        hipLaunchKernelGGL((prefill_kernel<D, QW, 2, DIRECT, true>), grid, dim3(64 * QW), 0, stream, p);
+        hipLaunchKernelGGL((prefill_kernel<D, kQW, 2, DIRECT, true>), grid, dim3(64 * kQW), 0, stream, p);
     else
-        hipLaunchKernelGGL((prefill_kernel<D, QW, 2, DIRECT, false>), grid, dim3(64 * QW), 0, stream, p);
+        hipLaunchKernelGGL((prefill_kernel<D, kQW, 2, DIRECT, false>), grid, dim3(64 * kQW), 0, stream, p);
 }
 
 template <int D>
-void launch_attention(const PrefillParams &p, int qw, bool direct, dim3 grid, hipStream_t stream) {
-    if (qw == 8)
-        direct ? launch_attention<D, 8, true>(p, grid, stream) : launch_attention<D, 8, false>(p, grid, stream);
-    else
-        direct ? launch_attention<D, 4, true>(p, grid, stream) : launch_attention<D, 4, false>(p, grid, stream);
+void launch_attention(const PrefillParams &p, bool direct, dim3 grid, hipStream_t stream) {
+    direct ? launch_attention<D, true>(p, grid, stream) : launch_attention<D, false>(p, grid, stream);
 }
 
 }  // namespace
 
-bool prefill_is_direct(const PrefillParams &p) {
-    return p.n_heads == p.n_kv && p.n_tok <= 32 * prefill_waves(p);
-}
+bool prefill_is_direct(const PrefillParams &p) { return p.n_heads == p.n_kv && p.n_tok <= 32 * kQW; }
 
 bool launch_prefill(const PrefillParams &p, hipStream_t stream) {
     if (p.g.head_dim != 128 && p.g.head_dim != 64) return false;
@@ -753,13 +746,12 @@ bool launch_prefill(const PrefillParams &p, hipStream_t stream) {
         hipLaunchKernelGGL(stage_kernel, dim3((unsigned) ((stage_threads + 255) / 256)), dim3(256), 0,
                            stream, p);
     }
-    const int qw = prefill_waves(p);
-    const int qt = 32 * qw;
+    const int qt = 32 * kQW;
     const dim3 grid((unsigned) ((int64_t) p.n_batch * p.n_heads * ((p.n_tok + qt - 1) / qt)));
     if (p.g.head_dim == 128)
-        launch_attention<128>(p, qw, direct, grid, stream);
+        launch_attention<128>(p, direct, grid, stream);
     else
-        launch_attention<64>(p, qw, direct, grid, stream);
+        launch_attention<64>(p, direct, grid, stream);
     if (!direct) {
         const int commit_threads = p.n_batch * p.n_tok * p.n_kv * nblk;
         hipLaunchKernelGGL(commit_kernel, dim3((unsigned) ((commit_threads + 255) / 256)), dim3(256), 0,
