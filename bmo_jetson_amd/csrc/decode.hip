@@ -562,11 +562,13 @@ struct Shape {
 // Workgroup shape per call: one wave per (entry, head) unit with two groups
 // of loads in flight when there are enough units to fill the chip (measured
 // best over sustained runs of BASELINE config 3), else enough waves per unit
-// for about 512 waves in all.  BMO_ATTN_SHAPE = "nw,pf" overrides the choice (tuning;
-// unknown shapes fall back to the default).
-Shape pick_shape(int64_t units, int n_groups) {
+// for about 512 waves in all.  Below 128 units a plain decode uses 4 waves
+// per unit and a fused one 8 (B=1, 32 units: 5.48 vs 5.68 us plain, 6.05 vs
+// 6.12 us fused, where wave 0 takes the new token).  BMO_ATTN_SHAPE = "nw,pf"
+// overrides the choice (tuning; unknown shapes fall back to the default).
+Shape pick_shape(int64_t units, int n_groups, bool fused) {
     Shape s{1, 2};
-    if (units < 128) s = Shape{8, 1};
+    if (units < 128) s = fused ? Shape{8, 1} : Shape{4, 1};
     else if (units < 256) s = Shape{4, 1};
     else if (units < 512) s = Shape{2, 1};
     while (s.nw > 1 && s.nw > n_groups) s.nw /= 2;  // no more waves than groups
@@ -601,7 +603,7 @@ bool launch_shape(const DecodeParams &p, bool fused, hipStream_t stream, const S
 bool launch_decode(const DecodeParams &p, bool fused, hipStream_t stream) {
     const int64_t units = (int64_t) p.n_batch * p.n_heads;
     if (units <= 0) return true;
-    const Shape s = pick_shape(units, p.g.n_groups);
+    const Shape s = pick_shape(units, p.g.n_groups, fused);
     if (p.g.head_dim == 128) {
         if (!launch_shape<128>(p, fused, stream, s)) launch_variant<128, 1, 1>(p, fused, stream);
     } else if (p.g.head_dim == 64) {
