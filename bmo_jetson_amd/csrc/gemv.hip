@@ -63,9 +63,10 @@ __device__ __forceinline__ uint32_t f32_to_f16(float x) {
 
 }  // namespace
 
-template <int R>
+template <int R, int PFD>
 __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
     constexpr int NT = 512;
+    constexpr int NB = PFD + 1;  // weight buffers: PFD iterations in flight
     extern __shared__ __align__(16) uint8_t smem[];
     const int nblk = p.cols / 32;
     const int npairs = nblk / 2;
@@ -77,11 +78,14 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
     const int wave = threadIdx.x >> 6;
     const int64_t row_bytes = (int64_t) nblk * 18;
     // Work of a wave: chunks of R consecutive rows, c = wave id, + stride,
-    // ..., each in n_it pair-iterations; the loads of the next (chunk,
-    // iteration) are in flight while the current one is multiplied.
+    // ..., each in n_it pair-iterations, n_pos (chunk, iteration) positions
+    // in all; the loads of the next PFD positions are in flight while the
+    // current one is multiplied.
     const int n_it = (npairs + 63) / 64;
     const int n_chunks = (p.rows + R - 1) / R;
     const int stride = gridDim.x * (NT / 64);
+    const int c0 = blockIdx.x * (NT / 64) + wave;
+    const int n_pos = (c0 < n_chunks ? (n_chunks - 1 - c0) / stride + 1 : 0) * n_it;
 
     // This lane's block pair of iteration it of chunk c (clamped to the
     // matrix: loads past the end read its last pair and are never used).
@@ -98,9 +102,21 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
             w[r][8] = src[8];
         }
     };
-    int c = blockIdx.x * (NT / 64) + wave;
-    int it = 0;
-    uint32_t wcur[R][9];
+    // load head: the next position to fetch.  Past the wave's end it
+    // re-reads the wave's own last position (every position issues the same
+    // loads, so the waits stay exact, and the extra reads hit lines this
+    // wave has just read rather than one line all waves would share).
+    const int c_last = n_pos > 0 ? c0 + (n_pos / n_it - 1) * stride : n_chunks - 1;
+    int lc = c0, lit = 0;
+    auto load_next = [&](uint32_t (&w)[R][9]) {
+        const bool past = lc > c_last;
+        load_pairs(past ? c_last : lc, past ? n_it - 1 : lit, w);
+        if (++lit == n_it) {
+            lit = 0;
+            lc += stride;
+        }
+    };
+    uint32_t wb[NB][R][9];
 
     // Activation row -> Q8_1 in LDS.  Thread t: block t/4 (+128 k), elements
     // 8 (t%4) .. 8 (t%4) + 7.  The first pass's x loads go out before the
@@ -113,7 +129,10 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
         const float *xb = p.x + b * 32;
         const float4 u = *reinterpret_cast<const float4 *>(xb + 8 * part);
         const float4 v = *reinterpret_cast<const float4 *>(xb + 8 * part + 4);
-        if (base == 0) load_pairs(min(c, n_chunks - 1), 0, wcur);
+        if (base == 0) {
+#pragma unroll
+            for (int j = 0; j < PFD; ++j) load_next(wb[j]);
+        }
         const float x8[8] = {u.x, u.y, u.z, u.w, v.x, v.y, v.z, v.w};
         float amax = 0.0f;
 #pragma unroll
@@ -160,14 +179,9 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-    while (c < n_chunks) {
-        int c2 = c, it2 = it + 1;
-        if (it2 == n_it) {
-            it2 = 0;
-            c2 = c + stride;
-        }
-        uint32_t wnext[R][9];
-        load_pairs(min(c2, n_chunks - 1), it2, wnext);  // unconditional: exact load waits
+    // compute tail: position k is (chunk c, iteration it)
+    int c = c0, it = 0;
+    auto multiply = [&](const uint32_t (&wcur)[R][9]) {
         const int pr = it * 64 + lane;
         if (pr < npairs) {
             const int b0 = 2 * pr;
@@ -210,12 +224,20 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
                 acc[r] = 0.0f;
             }
         }
+        if (++it == n_it) {
+            it = 0;
+            c += stride;
+        }
+    };
+    // Buffer of position k: k % NB.  Each step refills the buffer freed by
+    // the step before with position k + PFD (unconditional loads), then
+    // multiplies position k.
+    for (int k = 0; k < n_pos; k += NB) {
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-            for (int k = 0; k < 9; ++k) wcur[r][k] = wnext[r][k];
-        c = c2;
-        it = it2;
+        for (int u = 0; u < NB; ++u) {
+            load_next(wb[(u + PFD) % NB]);
+            if (k + u < n_pos) multiply(wb[u]);
+        }
     }
 }
 
@@ -233,7 +255,10 @@ void launch_rows(const GemvParams &p, hipStream_t stream) {
     int cap = 256;
     if (const char *e = std::getenv("BMO_GEMV_WGS")) cap = std::max(1, std::atoi(e));
     wgs = std::min(wgs, cap);
-    hipLaunchKernelGGL((gemv_kernel<R>), dim3((unsigned) wgs), dim3(512), gemv_lds_bytes(p.cols), stream,
+    // One position in flight beside the one being multiplied: 2, 3 and 4
+    // were measured slower at every shape (QKV 8.06 / 9.57 / 9.85 us against
+    // 7.62; out-proj 5.29 / 6.43 / 7.23 against 4.50).
+    hipLaunchKernelGGL((gemv_kernel<R, 1>), dim3((unsigned) wgs), dim3(512), gemv_lds_bytes(p.cols), stream,
                        p);
 }
 
