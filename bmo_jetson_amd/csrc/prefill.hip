@@ -11,8 +11,11 @@
 // (src/bmo_cuda_kernels.cu:739-747) extended to a causal chunk.
 //
 // The chunk overwrites slots that its own early queries still read (query 0
-// needs positions back to pos0 - n_ctx + 1), so one call runs three kernels
-// in stream order:
+// needs positions back to pos0 - n_ctx + 1).  With one query head per kv
+// head and at most 256 tokens, one workgroup reads each ring stripe: it
+// quantizes the chunk into LDS, attends, and writes the chunk's blocks into
+// the ring after its last tile (one kernel).  Otherwise one call runs three
+// kernels in stream order:
 //   stage_kernel   quantizes the chunk's bf16 K/V into a staging stripe with
 //                  the ring's group layout (slot i = chunk token i);
 //   prefill_kernel attention over the ring and the staged chunk;
@@ -20,13 +23,14 @@
 //
 // prefill_kernel: a workgroup of QW waves serves 16*QB*QW queries of one
 // (entry, head); each wave owns QB blocks of 16, so every K and V operand it
-// reads from LDS feeds QB matrix instructions.  Keys stream through two LDS
-// buffers in tiles of 32 positions: every thread fetches its share of the
-// Q4_0 bytes of the tile 3 ahead into registers while the waves compute the
-// current tile, then dequantizes the oldest fetched tile into the free buffer (K and V row-major) as
-// the fp16 value (code - 8) * d; one barrier per tile.  A wave
-// skips tiles that hold no key its queries may see.  Each wave computes
-// S^T = K Q^T with
+// reads from LDS feeds QB matrix instructions.  Keys stream through four LDS
+// buffers in tiles of 32 positions: every thread holds its share of the Q4_0
+// bytes of the next 7 tiles in registers and dequantizes the oldest two into
+// free buffers (K and V row-major) as the fp16 value (code - 8) * d; one
+// barrier publishes each pair of tiles.  A wave skips tiles that hold no key
+// its queries may see, and the tiles are paired so that, where the causal
+// and window masks allow, the two tiles of a pair are seen by different
+// waves.  Each wave computes S^T = K Q^T with
 // v_mfma_f32_16x16x32_f16 (the D layout of S^T puts 8 keys of one query in a
 // lane, exactly the A layout the P.V product needs), runs an online softmax
 // in the log2 domain and accumulates O += P V with the same instruction, its
@@ -218,7 +222,7 @@ __global__ __launch_bounds__(256) void commit_kernel(PrefillParams p) {
 // ring after its last tile, when no wave reads the old slots any more; no
 // stage or commit kernel runs.
 template <int D, int QW, int QB, bool DIRECT, bool ALIGNED>
-__global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams p) {
+__global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams p) {
     constexpr int NBLK = D / kQK;
     // LDS rows (fp16): K rows padded to 68 dwords so that the 16 lanes of an
     // operand read (16 keys, one 16-byte chunk each) hit 16 distinct 4-bank
@@ -286,6 +290,25 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams 
     const int c_start = pos0 + ((max(k_lo, pos0) - pos0) & ~(kTK - 1));
     const int n_tiles = n_rt + (p_last - c_start) / kTK + 1;
     auto tile_t0 = [&](int T) { return T < n_rt ? r_start + T * kTK : c_start + (T - n_rt) * kTK; };
+    // Processing order.  Wave w's queries start at p_first + 32w, so ring
+    // tile r is seen only by waves w <= r + beta (older keys leave the early
+    // waves' windows last) and chunk tile c only by waves w >= c - delta
+    // (causality).  Ring tile r and chunk tile r + gam are therefore seen by
+    // disjoint sets of waves; processing them as the two tiles of one
+    // barrier period lets each wave multiply one of them instead of some
+    // wave multiplying both.  The first 2M tiles alternate ring r / chunk
+    // r + gam, the rest follow in index order.  (Any order gives the same
+    // result up to rounding: the softmax is online.)
+    const int gam = (r_start + kTK - 2 - p_first + n_ctx) / kTK + 1 + (p_first - c_start) / kTK;
+    const int n_pair = max(0, min(n_rt, n_tiles - n_rt - gam));
+    // (selects, not branches: the callers' blocks stay whole)
+    auto tile_of = [&](int i) {
+        const int paired = (i & 1) ? n_rt + (i >> 1) + gam : (i >> 1);
+        const int j = i - 2 * n_pair;             // position among the unpaired tiles
+        const int jc = j - (n_rt - n_pair);       // ... among the unpaired chunk tiles
+        const int rest = j < n_rt - n_pair ? n_pair + j : n_rt + (jc < gam ? jc : jc + n_pair);
+        return i < 2 * n_pair ? paired : rest;    // padding positions map to themselves
+    };
     const uint8_t *ring = p.base + p.g.stripe_offset(p.layer, sid, kvh);
     const uint8_t *stage = p.stage + p.sg.stripe_offset(0, b, kvh);
     const uint32_t ring_gs = (uint32_t) p.g.group_stride;
@@ -326,27 +349,26 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams 
     static_assert((PF + 1) % NBUF == 0, "the unrolled slot must determine the LDS buffer");
     uint2 raw[PF + 1][IPT];
     uint32_t rawd[PF + 1][IPT];
-    int f_tile = 0;                  // next tile to fetch
-    int f_slot = r_start % n_ctx;    // its ring slot, while it is a ring tile
+    int f_next = 0;                        // next position in processing order to fetch
+    const int r_slot = r_start % n_ctx;    // ring slot of ring tile 0
     auto fetch = [&](uint2 (&rw)[IPT], uint32_t (&rd)[IPT]) {
-        const int T = f_tile++;
+        const int T = tile_of(f_next++);
         const bool ring_t = T < n_rt;
+        // a ring tile's first slot (r_start + 32 T) % n_ctx; 32 T <= n_ctx
+        // + 29, so one subtraction suffices when n_ctx is a multiple of 32
+        int slot0 = r_slot + T * kTK;
+        if (slot0 >= n_ctx) slot0 -= n_ctx;
+        if (!ALIGNED && slot0 >= n_ctx) slot0 %= n_ctx;
         const bool staged_t = !DIRECT && !ring_t && T < n_tiles;
         // Scalar: the slot group of the tile's first key (ALIGNED: a ring
         // tile's slots t0 % n_ctx .. +31 never wrap) and the last group the
         // tile may address; keys past the staged chunk clamp to its last
         // group, and a tile with no keys to load reads group 0 only, so
         // every address stays inside the stripe.
-        const int g_first = staged_t ? (tile_t0(T) - pos0) / G : ring_t ? f_slot / G : 0;
+        const int g_first = staged_t ? (tile_t0(T) - pos0) / G : ring_t ? slot0 / G : 0;
         const int g_last = staged_t ? p.sg.n_groups - 1 : ring_t ? p.g.n_groups - 1 : 0;
         const uint8_t *gsrc = staged_t ? stage : ring;
         const uint32_t gs = staged_t ? stage_gs : ring_gs;
-        const int slot0 = f_slot;
-        if (ring_t) {
-            f_slot += kTK;
-            if (f_slot >= n_ctx) f_slot -= n_ctx;
-            if (!ALIGNED && f_slot >= n_ctx) f_slot %= n_ctx;
-        }
 #pragma unroll
         for (int j = 0; j < IPT; ++j) {
             const uint8_t *gp = gsrc + (uint64_t) (uint32_t) min(g_first + it_grp[j], g_last) * gs;
@@ -362,11 +384,15 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams 
                     so = it_scale[j] + (row - (uint32_t) (it_key[j] % G)) * (NBLK * 4);
                 }
             }
-            rw[j] = *reinterpret_cast<const uint2 *>(gp + co);
-            // the whole scale dword: a 16-bit load would be zero-extended
-            // into a copy that hipcc places at the loop's back edge, waiting
-            // for the load there
-            rd[j] = *reinterpret_cast<const uint32_t *>(gp + so);
+            // waves past the tile's items (16 waves, 8 items' worth) issue
+            // no loads; the test is wave-uniform
+            if (j * NTHR + wave * 64 < ITEMS) {
+                rw[j] = *reinterpret_cast<const uint2 *>(gp + co);
+                // the whole scale dword: a 16-bit load would be zero-extended
+                // into a copy that hipcc places at the loop's back edge,
+                // waiting for the load there
+                rd[j] = *reinterpret_cast<const uint32_t *>(gp + so);
+            }
         }
     };
     // Dequantizes fetched items of tile T into LDS buffer `buf`: K and V
@@ -628,17 +654,18 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams 
         }
         lds_barrier();
     };
-    // Tile T lives in raw slot T % (PF + 1) and LDS buffer T % NBUF; its
-    // loads are issued PF tiles ahead, into the slot of tile T - 1.  Buffer
-    // safety: the barrier of a tile pair follows every wave's multiplication
-    // of the pair before, so writing a buffer NBUF tiles later is safe.
+    // The tile at position i of the processing order lives in raw slot
+    // i % (PF + 1) and LDS buffer i % NBUF; its loads are issued PF positions
+    // ahead, into the slot of position i - 1.  Buffer safety: the barrier of
+    // a tile pair follows every wave's multiplication of the pair before, so
+    // writing a buffer NBUF positions later is safe.
     if constexpr (DIRECT) quantize_chunk();
     for (int base = 0; base < n_tiles; base += PF + 1) {
 #pragma unroll
         for (int u = 0; u <= PF; u += TPB) {
 #pragma unroll
             for (int k = 0; k < TPB; ++k)
-                deposit((u + k) % NBUF, base + u + k, raw[u + k], rawd[u + k]);
+                deposit((u + k) % NBUF, tile_of(base + u + k), raw[u + k], rawd[u + k]);
             lds_barrier();  // these TPB buffers are complete
 #pragma unroll
             for (int k = 0; k < TPB; ++k) {
@@ -646,7 +673,7 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams 
                 fetch(raw[nxt], rawd[nxt]);
             }
 #pragma unroll
-            for (int k = 0; k < TPB; ++k) compute((u + k) % NBUF, base + u + k);
+            for (int k = 0; k < TPB; ++k) compute((u + k) % NBUF, tile_of(base + u + k));
         }
     }
 
@@ -712,20 +739,35 @@ __global__ __launch_bounds__(64 * QW, 8 / QW) void prefill_kernel(PrefillParams 
 
 namespace {
 
-// 8 waves x 32 queries: one workgroup per 256 queries of a head.  Smaller
-// workgroups for short chunks (4 waves below 129 tokens) were measured slower
-// whenever the ring holds history (64.6 vs 58.9 us at 16 tokens, 79.8 vs
-// 71.5 us at 128, cfg5 shape): the window's tiles dominate, and 8 waves
-// share their dequantization.
-constexpr int kQW = 8;
+// One workgroup per 256 queries of a head, in one of two shapes:
+//   16 waves x 16 queries (QB = 1): 4 waves on each SIMD (128 VGPRs each),
+//      so one wave's LDS and matrix latencies overlap another's work.  Used
+//      for the direct path with n_ctx a multiple of 32 (the temporal ring):
+//      at cfg5 it measured 95.5 vs 99.6 us (ring history full) and 55.6 vs
+//      61.1 us (empty) against the other shape;
+//   8 waves x 32 queries (QB = 2): each K/V operand read feeds two matrix
+//      instructions.  Used for the staged path and for other ring sizes, whose
+//      kernels spill registers in the 128-VGPR shape.
+// Smaller workgroups for short chunks (4 waves below 129 tokens) were
+// measured slower whenever the ring holds history: the window's tiles
+// dominate, and all waves share their dequantization.
+constexpr int kQT = 256;  // queries per workgroup
+
+template <int D, int QW, int QB, bool DIRECT, bool ALIGNED>
+void launch_shape(const PrefillParams &p, dim3 grid, hipStream_t stream) {
+    static_assert(16 * QB * QW == kQT, "every shape serves kQT queries");
+    hipLaunchKernelGGL((prefill_kernel<D, QW, QB, DIRECT, ALIGNED>), grid, dim3(64 * QW), 0, stream, p);
+}
 
 template <int D, bool DIRECT>
 void launch_attention(const PrefillParams &p, dim3 grid, hipStream_t stream) {
     // ring tiles 32 slots wide never wrap when n_ctx is a multiple of 32
-    if (p.g.n_ctx % kTK == 0)
-        hipLaunchKernelGGL((prefill_kernel<D, kQW, 2, DIRECT, true>), grid, dim3(64 * kQW), 0, stream, p);
+    if (p.g.n_ctx % kTK != 0)
+        launch_shape<D, 8, 2, DIRECT, false>(p, grid, stream);
+    else if constexpr (DIRECT)
+        launch_shape<D, 16, 1, DIRECT, true>(p, grid, stream);
     else
-        hipLaunchKernelGGL((prefill_kernel<D, kQW, 2, DIRECT, false>), grid, dim3(64 * kQW), 0, stream, p);
+        launch_shape<D, 8, 2, DIRECT, true>(p, grid, stream);
 }
 
 template <int D>
@@ -735,7 +777,7 @@ void launch_attention(const PrefillParams &p, bool direct, dim3 grid, hipStream_
 
 }  // namespace
 
-bool prefill_is_direct(const PrefillParams &p) { return p.n_heads == p.n_kv && p.n_tok <= 32 * kQW; }
+bool prefill_is_direct(const PrefillParams &p) { return p.n_heads == p.n_kv && p.n_tok <= kQT; }
 
 bool launch_prefill(const PrefillParams &p, hipStream_t stream) {
     if (p.g.head_dim != 128 && p.g.head_dim != 64) return false;
@@ -746,7 +788,7 @@ bool launch_prefill(const PrefillParams &p, hipStream_t stream) {
         hipLaunchKernelGGL(stage_kernel, dim3((unsigned) ((stage_threads + 255) / 256)), dim3(256), 0,
                            stream, p);
     }
-    const int qt = 32 * kQW;
+    const int qt = kQT;
     const dim3 grid((unsigned) ((int64_t) p.n_batch * p.n_heads * ((p.n_tok + qt - 1) / qt)));
     if (p.g.head_dim == 128)
         launch_attention<128>(p, direct, grid, stream);
