@@ -24,10 +24,10 @@
 // prefill_kernel: a workgroup of QW waves serves 16*QB*QW queries of one
 // (entry, head); each wave owns QB blocks of 16, so every K and V operand it
 // reads from LDS feeds QB matrix instructions.  Keys stream through four LDS
-// buffers in tiles of 32 positions: every thread holds its share of the Q4_0
-// bytes of the next 7 tiles in registers and dequantizes the oldest two into
-// free buffers (K and V row-major) as the fp16 value (code - 8) * d; one
-// barrier publishes each pair of tiles.  A wave skips tiles that hold no key
+// buffers in tiles of 32 positions: each thread of the loading waves holds
+// its share of the Q4_0 bytes of the next 3 tiles in registers and
+// dequantizes the oldest two into free buffers (K and V row-major) as the
+// fp16 value (code - 8) * d; one barrier publishes each pair of tiles.  A wave skips tiles that hold no key
 // its queries may see, and the tiles are paired so that, where the causal
 // and window masks allow, the two tiles of a pair are seen by different
 // waves.  Each wave computes S^T = K Q^T with
@@ -52,6 +52,11 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
+
+template <bool B>
+struct BoolC {
+    static constexpr bool value = B;
+};
 
 constexpr int kTK = 32;          // keys per tile
 constexpr float kRescale = 8.0f; // lazy rescale threshold, log2 units
@@ -289,7 +294,9 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
     const int n_rt = k_lo < pos0 ? (pos0 - 1 - r_start) / kTK + 1 : 0;
     const int c_start = pos0 + ((max(k_lo, pos0) - pos0) & ~(kTK - 1));
     const int n_tiles = n_rt + (p_last - c_start) / kTK + 1;
-    auto tile_t0 = [&](int T) { return T < n_rt ? r_start + T * kTK : c_start + (T - n_rt) * kTK; };
+    // (helpers capture by value: a select between captured references can
+    // keep the closures in scratch memory, as noted at src_diff below)
+    auto tile_t0 = [=](int T) { return T < n_rt ? r_start + T * kTK : c_start + (T - n_rt) * kTK; };
     // Processing order.  Wave w's queries start at p_first + 32w, so ring
     // tile r is seen only by waves w <= r + beta (older keys leave the early
     // waves' windows last) and chunk tile c only by waves w >= c - delta
@@ -302,7 +309,7 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
     const int gam = (r_start + kTK - 2 - p_first + n_ctx) / kTK + 1 + (p_first - c_start) / kTK;
     const int n_pair = max(0, min(n_rt, n_tiles - n_rt - gam));
     // (selects, not branches: the callers' blocks stay whole)
-    auto tile_of = [&](int i) {
+    auto tile_of = [=](int i) {
         const int paired = (i & 1) ? n_rt + (i >> 1) + gam : (i >> 1);
         const int j = i - 2 * n_pair;             // position among the unpaired tiles
         const int jc = j - (n_rt - n_pair);       // ... among the unpaired chunk tiles
@@ -313,6 +320,15 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
     const uint8_t *stage = p.stage + p.sg.stripe_offset(0, b, kvh);
     const uint32_t ring_gs = (uint32_t) p.g.group_stride;
     const uint32_t stage_gs = (uint32_t) p.sg.group_stride;
+    // Staging minus ring: the fetch selects between the two sources as ring
+    // + (staged ? difference : 0).  (A select between two captured values
+    // becomes, once hipcc simplifies the lambda, a select between two
+    // addresses in its closure, which keeps the closure and everything it
+    // refers to in scratch memory.)
+    const int64_t src_diff = stage - ring;
+    const int32_t gs_diff = (int32_t) (stage_gs - ring_gs);
+    const int rg_last = p.g.n_groups - 1;                    // last group of a ring stripe
+    const int glast_diff = p.sg.n_groups - p.g.n_groups;    // ... staging minus ring
 
     // This thread's items: item j is (K/V, key, block, 8-byte half) =
     // (which, key, bb, hf) of every tile.  A wave's 64 items share `which`
@@ -344,8 +360,10 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
     // fetch issues its loads (tiles whose keys come from elsewhere -- DIRECT
     // chunk tiles, padding tiles past the end -- read the ring stripe's first
     // slots, which stay cached), so the number of loads in flight is the same
-    // on every path and the compiler's waits stay exact.
-    constexpr int PF = 7;
+    // on every path and the compiler's waits stay exact.  Depth: 3 tiles
+    // with 16 waves (4 per SIMD hide the rest; 84.0 vs 85.7 us at depth 7,
+    // cfg5), 7 with 8 waves.
+    constexpr int PF = QW >= 16 ? 3 : 7;
     static_assert((PF + 1) % NBUF == 0, "the unrolled slot must determine the LDS buffer");
     uint2 raw[PF + 1][IPT];
     uint32_t rawd[PF + 1][IPT];
@@ -366,9 +384,9 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
         // group, and a tile with no keys to load reads group 0 only, so
         // every address stays inside the stripe.
         const int g_first = staged_t ? (tile_t0(T) - pos0) / G : ring_t ? slot0 / G : 0;
-        const int g_last = staged_t ? p.sg.n_groups - 1 : ring_t ? p.g.n_groups - 1 : 0;
-        const uint8_t *gsrc = staged_t ? stage : ring;
-        const uint32_t gs = staged_t ? stage_gs : ring_gs;
+        const int g_last = (ring_t || staged_t) ? rg_last + (staged_t ? glast_diff : 0) : 0;
+        const uint8_t *gsrc = ring + (staged_t ? src_diff : 0);
+        const uint32_t gs = ring_gs + (uint32_t) (staged_t ? gs_diff : 0);
 #pragma unroll
         for (int j = 0; j < IPT; ++j) {
             const uint8_t *gp = gsrc + (uint64_t) (uint32_t) min(g_first + it_grp[j], g_last) * gs;
@@ -384,15 +402,11 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
                     so = it_scale[j] + (row - (uint32_t) (it_key[j] % G)) * (NBLK * 4);
                 }
             }
-            // waves past the tile's items (16 waves, 8 items' worth) issue
-            // no loads; the test is wave-uniform
-            if (j * NTHR + wave * 64 < ITEMS) {
-                rw[j] = *reinterpret_cast<const uint2 *>(gp + co);
-                // the whole scale dword: a 16-bit load would be zero-extended
-                // into a copy that hipcc places at the loop's back edge,
-                // waiting for the load there
-                rd[j] = *reinterpret_cast<const uint32_t *>(gp + so);
-            }
+            rw[j] = *reinterpret_cast<const uint2 *>(gp + co);
+            // the whole scale dword: a 16-bit load would be zero-extended
+            // into a copy that hipcc places at the loop's back edge, waiting
+            // for the load there
+            rd[j] = *reinterpret_cast<const uint32_t *>(gp + so);
         }
     };
     // Dequantizes fetched items of tile T into LDS buffer `buf`: K and V
@@ -469,10 +483,16 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
     // body has no per-tile condition around its loads.  The scheduling
     // barriers keep hipcc from hoisting later loads above earlier ones, so
     // that each wait covers the oldest loads only.
+    // Waves with dequantization items (all of them in the 8-wave shape, the
+    // first 8 in the 16-wave one) fetch and deposit; the others only
+    // multiply.  Wave-uniform.
+    const bool has_items = (IPT - 1) * NTHR + wave * 64 < ITEMS;
+    if (has_items) {
 #pragma unroll
-    for (int j = 0; j < PF; ++j) {
-        fetch(raw[j], rawd[j]);
-        __builtin_amdgcn_sched_barrier(0);
+        for (int j = 0; j < PF; ++j) {
+            fetch(raw[j], rawd[j]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
     }
     // DIRECT: this thread's blocks of the chunk's K and V (bf16), all in
     // flight at once
@@ -660,22 +680,36 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
     // a tile pair follows every wave's multiplication of the pair before, so
     // writing a buffer NBUF positions later is safe.
     if constexpr (DIRECT) quantize_chunk();
-    for (int base = 0; base < n_tiles; base += PF + 1) {
+    // The loop in two copies, so that the loading copy has its loads on
+    // every path and the compiler's waits count exactly (loads behind a
+    // branch turn every wait into a wait for all loads).
+    auto tile_loop = [&](auto loads) {
+        constexpr bool LOADS = decltype(loads)::value;
+        for (int base = 0; base < n_tiles; base += PF + 1) {
 #pragma unroll
-        for (int u = 0; u <= PF; u += TPB) {
+            for (int u = 0; u <= PF; u += TPB) {
+                if constexpr (LOADS) {
 #pragma unroll
-            for (int k = 0; k < TPB; ++k)
-                deposit((u + k) % NBUF, tile_of(base + u + k), raw[u + k], rawd[u + k]);
-            lds_barrier();  // these TPB buffers are complete
+                    for (int k = 0; k < TPB; ++k)
+                        deposit((u + k) % NBUF, tile_of(base + u + k), raw[u + k], rawd[u + k]);
+                }
+                lds_barrier();  // these TPB buffers are complete
+                if constexpr (LOADS) {
 #pragma unroll
-            for (int k = 0; k < TPB; ++k) {
-                const int nxt = (u + k + PF) % (PF + 1);
-                fetch(raw[nxt], rawd[nxt]);
+                    for (int k = 0; k < TPB; ++k) {
+                        const int nxt = (u + k + PF) % (PF + 1);
+                        fetch(raw[nxt], rawd[nxt]);
+                    }
+                }
+#pragma unroll
+                for (int k = 0; k < TPB; ++k) compute((u + k) % NBUF, tile_of(base + u + k));
             }
-#pragma unroll
-            for (int k = 0; k < TPB; ++k) compute((u + k) % NBUF, tile_of(base + u + k));
         }
-    }
+    };
+    if (has_items)
+        tile_loop(BoolC<true>{});
+    else
+        tile_loop(BoolC<false>{});
 
     if constexpr (DIRECT) {
         // The chunk's blocks into their ring slots (pos0 + i) % n_ctx.  Every
