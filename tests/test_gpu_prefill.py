@@ -77,6 +77,18 @@ def test_prefill_ring_sizes(gpu, n_ctx, pos0, n_tok, n_heads, n_kv):
     _run(gpu, m, 0, [(0, pos0)], n_tok, n_heads, seed=310 + n_ctx)
 
 
+@pytest.mark.parametrize("n_ctx,pos0,n_tok,n_heads,n_kv", [
+    (64, 200, 64, 4, 4),    # direct path, ring a multiple of 32 (16 waves x 16 queries)
+    (512, 700, 256, 2, 2),  # the same at the temporal ring's size, a full chunk
+    (64, 90, 40, 8, 2),     # staged path (4 query heads per kv head), aligned ring
+    (40, 90, 30, 4, 2),     # staged path, ring not a multiple of 32
+])
+def test_prefill_head_dim_64(gpu, n_ctx, pos0, n_tok, n_heads, n_kv):
+    m = Mirror(gpu, 1, 1, n_kv, 64, n_ctx)
+    m.fill_range(0, 0, 0, pos0, seed=400 + n_ctx)
+    _run(gpu, m, 0, [(0, pos0)], n_tok, n_heads, seed=410 + n_tok)
+
+
 def test_prefill_gqa_and_head_dim_64(gpu):
     m = Mirror(gpu, 1, 1, 2, 128, 96)
     m.fill_range(0, 0, 0, 150, seed=31)
