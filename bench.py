@@ -105,7 +105,9 @@ def time_steps(torch, launch_layer, n_layers, steps, warmup):
     `steps` replays between two torch.cuda.synchronize() calls with a HIP
     event pair recorded on the replay stream.  Returns ms per step; the mean
     launch duration is that over n_layers (it includes the small gaps between
-    the graph's kernels, so it is an upper bound on the kernel time)."""
+    the graph's kernels, so it is an upper bound on the kernel time).  Then
+    `steps` more replays, each between its own event pair, give the per-step
+    distribution (median, min, max), outside the timed region."""
     stream = torch.cuda.current_stream()
     for _ in range(warmup):
         for layer in range(n_layers):
@@ -127,8 +129,16 @@ def time_steps(torch, launch_layer, n_layers, steps, warmup):
         graph.replay()
     t1.record(stream)
     torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    ev[0].record(stream)
+    for i in range(steps):
+        graph.replay()
+        ev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    per_step = [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
     del graph
-    return t0.elapsed_time(t1) / steps
+    return ms, per_step
 
 
 def graph_us_per_call(torch, call, calls_per_graph, reps=5):
@@ -454,7 +464,7 @@ def main():
         else:
             ring.decode(layer, pos, q[layer], out[layer], H, stream=st)
 
-    ms_per_step = time_steps(torch, launch_layer, L, args.steps, args.warmup)
+    ms_per_step, per_step = time_steps(torch, launch_layer, L, args.steps, args.warmup)
     launch_ms = ms_per_step / L
     per_step_bytes = unit_bytes(H, D, W) * S * L
     if fused:
@@ -475,6 +485,9 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 4),
+        "step_ms_dist": {"median": round(float(np.median(per_step)), 4),
+                         "min": round(min(per_step), 4), "max": round(max(per_step), 4),
+                         "n": len(per_step), "note": "separate replays after the timed region"},
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
