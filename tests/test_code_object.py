@@ -10,7 +10,6 @@ code objects' metadata notes with ROCm's own tools (no GPU needed) and fails
 on any kernel with a private segment or a VGPR spill."""
 import os
 import re
-import shutil
 import subprocess
 
 import pytest
