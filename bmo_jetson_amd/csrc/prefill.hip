@@ -25,12 +25,12 @@
 // (entry, head); each wave owns QB blocks of 16, so every K and V operand it
 // reads from LDS feeds QB matrix instructions.  Keys stream through four LDS
 // buffers in tiles of 32 positions: each thread of the loading waves holds
-// its share of the Q4_0 bytes of the next 3 tiles in registers and
+// its share of the Q4_0 bytes of the next tiles in registers and
 // dequantizes the oldest two into free buffers (K and V row-major) as the
-// fp16 value (code - 8) * d; one barrier publishes each pair of tiles.  A wave skips tiles that hold no key
-// its queries may see, and the tiles are paired so that, where the causal
-// and window masks allow, the two tiles of a pair are seen by different
-// waves.  Each wave computes S^T = K Q^T with
+// fp16 value (code - 8) * d; one barrier publishes each pair of tiles.  A
+// wave skips tiles that hold no key its queries may see, and the tiles are
+// paired so that, where the causal and window masks allow, the two tiles of
+// a pair are seen by different waves.  Each wave computes S^T = K Q^T with
 // v_mfma_f32_16x16x32_f16 (the D layout of S^T puts 8 keys of one query in a
 // lane, exactly the A layout the P.V product needs), runs an online softmax
 // in the log2 domain and accumulates O += P V with the same instruction, its
@@ -297,15 +297,19 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
     // (helpers capture by value: a select between captured references can
     // keep the closures in scratch memory, as noted at src_diff below)
     auto tile_t0 = [=](int T) { return T < n_rt ? r_start + T * kTK : c_start + (T - n_rt) * kTK; };
-    // Processing order.  Wave w's queries start at p_first + 32w, so ring
-    // tile r is seen only by waves w <= r + beta (older keys leave the early
-    // waves' windows last) and chunk tile c only by waves w >= c - delta
-    // (causality).  Ring tile r and chunk tile r + gam are therefore seen by
-    // disjoint sets of waves; processing them as the two tiles of one
-    // barrier period lets each wave multiply one of them instead of some
-    // wave multiplying both.  The first 2M tiles alternate ring r / chunk
-    // r + gam, the rest follow in index order.  (Any order gives the same
-    // result up to rounding: the softmax is online.)
+    // Processing order.  A query at position P sees ring tile r only while
+    // P <= (last key of r) + n_ctx - 1, and chunk tile c only from P >=
+    // (first key of c) on: ring tiles are seen by the early waves, chunk
+    // tiles by the late ones.  gam puts the first key of chunk tile r + gam
+    // past the last query that sees ring tile r.  That key is a multiple of
+    // 32 positions after p_first, and each wave's first query is a multiple
+    // of its 16 or 32 queries after p_first, so a wave that sees the chunk
+    // tile starts at or after it and cannot see the ring tile: processing
+    // them as the two tiles of one barrier period lets each wave multiply
+    // one of them instead of some wave multiplying both.  The first
+    // 2 n_pair tiles alternate ring r / chunk r + gam, the rest follow in
+    // index order.  (Any order gives the same result up to rounding: the
+    // softmax is online.)
     const int gam = (r_start + kTK - 2 - p_first + n_ctx) / kTK + 1 + (p_first - c_start) / kTK;
     const int n_pair = max(0, min(n_rt, n_tiles - n_rt - gam));
     // (selects, not branches: the callers' blocks stay whole)
