@@ -70,6 +70,8 @@ def test_prefill_parity(gpu, pos0, n_tok):
     (72, 100, 60, 8, 2),    # staged chunk (4 query heads per kv head)
     (100, 1000, 100, 4, 4),
     (96, 70, 9, 4, 4),      # ring tiles aligned, last one partial
+    (1024, 3000, 256, 2, 2),   # a 1024-slot ring: 33 ring tiles, several loop passes
+    (1024, 3001, 200, 2, 2),   # the same with the chunk start off the 32-slot grid
 ])
 def test_prefill_ring_sizes(gpu, n_ctx, pos0, n_tok, n_heads, n_kv):
     m = Mirror(gpu, 1, 1, n_kv, 128, n_ctx)
