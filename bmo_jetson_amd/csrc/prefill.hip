@@ -60,8 +60,9 @@ struct BoolC {
 
 constexpr int kTK = 32;          // keys per tile
 constexpr float kRescale = 8.0f; // lazy rescale threshold, log2 units
-// Running-max floor: finite, so a masked score (-inf) gives exp2(-inf - m)
-// = 0 with no select, and far below any real score.
+// Running-max floor: far below any real score, so a query's first finite
+// score always triggers a rescale, and finite, so a masked score (-inf)
+// never does (and its weight exp2(-inf) is 0 with no select).
 constexpr float kMaxFloor = -1.0e30f;
 
 __device__ __forceinline__ float bf16_to_f32(uint32_t bits) {
@@ -542,12 +543,23 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
     // times a ones operand, whose every column is the weight sum of a query
     // row; both use the D layout (lane l: column l % 16, queries 4c + v), so
     // the final division needs no cross-lane exchange.
-    float m[QB];
+    // Softmax state per query block (log2 domain).  The S^T products start
+    // from -off, a per-query offset, so they come out as score - off; dl =
+    // running max - off.  off is 0 until a query's first rescale, which
+    // sets off to the running max (dl = 0) and is exact then because the
+    // products were taken from 0.  A rescale happens whenever a score
+    // exceeds the running max by kRescale, so after the test below every
+    // query with a finite score has dl = 0 and its weights are exp2 of the
+    // products themselves; a query still at the floor has only -inf scores,
+    // whose weights are 0 either way.
+    float dl[QB];
+    float4_t cneg[QB];  // -off for each of the lane's four products
     float4_t acc[QB][NT];
     float4_t accl[QB];
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
-        m[qb] = kMaxFloor;
+        dl[qb] = kMaxFloor;
+        cneg[qb] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
         accl[qb] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int t = 0; t < NT; ++t) acc[qb][t] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
@@ -565,7 +577,7 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
 #pragma unroll
         for (int sub = 0; sub < 2; ++sub) {
 #pragma unroll
-            for (int qb = 0; qb < QB; ++qb) s[qb][sub] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int qb = 0; qb < QB; ++qb) s[qb][sub] = cneg[qb];
 #pragma unroll
             for (int bb = 0; bb < NBLK; ++bb) {
                 const half8_t kop = *reinterpret_cast<const half8_t *>(
@@ -602,18 +614,25 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
         half8_t pop[QB];
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
-            // This lane's 8 scores against the running max; the exact
-            // per-query maximum (a cross-lane reduction) is only needed when
-            // some score exceeds the running max by kRescale.
+            // This lane's 8 scores (relative to off) against the running
+            // max; the exact per-query maximum (a cross-lane reduction) is
+            // only needed when some score exceeds the running max by
+            // kRescale.
             float tmax = vmax(vmax(vmax(s[qb][0][0], s[qb][0][1]), s[qb][0][2]),
                               vmax(vmax(vmax(s[qb][0][3], s[qb][1][0]), s[qb][1][1]),
                                    vmax(vmax(s[qb][1][2], s[qb][1][3]), -INFINITY)));
-            if (__any(tmax > m[qb] + kRescale)) {
+            if (__any(tmax > dl[qb] + kRescale)) {
                 tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
                 tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-                const bool need = tmax > m[qb] + kRescale;
-                const float alpha = need ? __builtin_amdgcn_exp2f(m[qb] - tmax) : 1.0f;
-                m[qb] = need ? tmax : m[qb];
+                const bool need = tmax > dl[qb] + kRescale;
+                const float alpha = need ? __builtin_amdgcn_exp2f(dl[qb] - tmax) : 1.0f;
+                // the new running max becomes off: shift it, and this tile's
+                // products, by tmax
+                const float shift = need ? tmax : 0.0f;
+                dl[qb] = need ? 0.0f : dl[qb];
+                cneg[qb] -= shift;
+#pragma unroll
+                for (int sub = 0; sub < 2; ++sub) s[qb][sub] -= shift;
                 // acc rows are queries 4c + v: fetch their alphas from lanes 4c + v
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
@@ -627,7 +646,7 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
             for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
                 for (int v = 0; v < 4; ++v)
-                    pop[qb][sub * 4 + v] = (_Float16) __builtin_amdgcn_exp2f(s[qb][sub][v] - m[qb]);
+                    pop[qb][sub * 4 + v] = (_Float16) __builtin_amdgcn_exp2f(s[qb][sub][v]);
             accl[qb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pop[qb], ones, accl[qb], 0, 0, 0);
         }
         // O += P V: B operand lane l = column t*16 + n of the tile, keys
