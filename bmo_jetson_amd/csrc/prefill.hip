@@ -367,7 +367,7 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
     // slots, which stay cached), so the number of loads in flight is the same
     // on every path and the compiler's waits stay exact.  Depth: 3 tiles
     // with 16 waves (4 per SIMD hide the rest; 84.0 vs 85.7 us at depth 7,
-    // cfg5), 7 with 8 waves.
+    // cfg5, and no register spills in any instantiation), 7 with fewer.
     constexpr int PF = QW >= 16 ? 3 : 7;
     static_assert((PF + 1) % NBUF == 0, "the unrolled slot must determine the LDS buffer");
     uint2 raw[PF + 1][IPT];
@@ -488,8 +488,8 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
     // body has no per-tile condition around its loads.  The scheduling
     // barriers keep hipcc from hoisting later loads above earlier ones, so
     // that each wait covers the oldest loads only.
-    // Waves with dequantization items (all of them in the 8-wave shape, the
-    // first 8 in the 16-wave one) fetch and deposit; the others only
+    // Waves with dequantization items (the first ITEMS / 64: 8 of 16 at
+    // head_dim 128, 4 at head_dim 64) fetch and deposit; the others only
     // multiply.  Wave-uniform.
     const bool has_items = (IPT - 1) * NTHR + wave * 64 < ITEMS;
     if (has_items) {
@@ -796,35 +796,27 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
 
 namespace {
 
-// One workgroup per 256 queries of a head, in one of two shapes:
-//   16 waves x 16 queries (QB = 1): 4 waves on each SIMD (128 VGPRs each),
-//      so one wave's LDS and matrix latencies overlap another's work.  Used
-//      for the direct path with n_ctx a multiple of 32 (the temporal ring):
-//      at cfg5 it measured 95.5 vs 99.6 us (ring history full) and 55.6 vs
-//      61.1 us (empty) against the other shape;
-//   8 waves x 32 queries (QB = 2): each K/V operand read feeds two matrix
-//      instructions.  Used for the staged path and for other ring sizes, whose
-//      kernels spill registers in the 128-VGPR shape.
+// One workgroup per 256 queries of a head: 16 waves x 16 queries (QB = 1),
+// 4 waves on each SIMD (at most 128 VGPRs each), so one wave's LDS and
+// matrix latencies overlap another's work.  Against 8 waves x 32 queries
+// (QB = 2, each K/V operand read feeding two matrix instructions), measured
+// at cfg5: 95.5 vs 99.6 us (ring history full), 55.6 vs 61.1 us (empty);
+// GQA 4:1, 256 tokens: 84-85 vs 91-94 us; 512-token chunks: 91-93 vs
+// 99-100 us; head_dim 64 GQA 4:1 on an 8-slot ring: 13.9 vs 16.7 us.
 // Smaller workgroups for short chunks (4 waves below 129 tokens) were
 // measured slower whenever the ring holds history: the window's tiles
 // dominate, and all waves share their dequantization.
-constexpr int kQT = 256;  // queries per workgroup
-
-template <int D, int QW, int QB, bool DIRECT, bool ALIGNED>
-void launch_shape(const PrefillParams &p, dim3 grid, hipStream_t stream) {
-    static_assert(16 * QB * QW == kQT, "every shape serves kQT queries");
-    hipLaunchKernelGGL((prefill_kernel<D, QW, QB, DIRECT, ALIGNED>), grid, dim3(64 * QW), 0, stream, p);
-}
+constexpr int kQW = 16;
+constexpr int kQB = 1;
+constexpr int kQT = 16 * kQB * kQW;  // queries per workgroup
 
 template <int D, bool DIRECT>
 void launch_attention(const PrefillParams &p, dim3 grid, hipStream_t stream) {
     // ring tiles 32 slots wide never wrap when n_ctx is a multiple of 32
-    if (p.g.n_ctx % kTK != 0)
-        launch_shape<D, 8, 2, DIRECT, false>(p, grid, stream);
-    else if constexpr (DIRECT)
-        launch_shape<D, 16, 1, DIRECT, true>(p, grid, stream);
+    if (p.g.n_ctx % kTK == 0)
+        hipLaunchKernelGGL((prefill_kernel<D, kQW, kQB, DIRECT, true>), grid, dim3(64 * kQW), 0, stream, p);
     else
-        launch_shape<D, 8, 2, DIRECT, true>(p, grid, stream);
+        hipLaunchKernelGGL((prefill_kernel<D, kQW, kQB, DIRECT, false>), grid, dim3(64 * kQW), 0, stream, p);
 }
 
 template <int D>
