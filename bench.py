@@ -298,7 +298,7 @@ def bench_prefill(torch, reps=10):
 
 
 def bench_gemv(torch, reps=50):
-    """SURVEY next row 2: the Q4_0 x Q8_1 GEMV around attention, at the
+    """The Q4_0 x Q8_1 GEMV of the projections around attention, at the
     reference's bench shapes (src/bmo_kernel_bench.cu:387-389) and the output
     projection, x = 0.5 as in the reference bench.  Per call from HIP-graph
     replays; GB/s counts the Q4_0 weight bytes (18 per 32 elements)."""
