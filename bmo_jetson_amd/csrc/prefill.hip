@@ -715,15 +715,17 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
 #pragma unroll
                     for (int k = 0; k < TPB; ++k)
                         deposit((u + k) % NBUF, tile_of(base + u + k), raw[u + k], rawd[u + k]);
-                }
-                lds_barrier();  // these TPB buffers are complete
-                if constexpr (LOADS) {
+                    // the next tiles' loads refill the registers just
+                    // dequantized; issued before the barrier, they are in
+                    // flight while the waves wait (the barrier waits for LDS
+                    // operations only)
 #pragma unroll
                     for (int k = 0; k < TPB; ++k) {
                         const int nxt = (u + k + PF) % (PF + 1);
                         fetch(raw[nxt], rawd[nxt]);
                     }
                 }
+                lds_barrier();  // these TPB buffers are complete
 #pragma unroll
                 for (int k = 0; k < TPB; ++k) compute((u + k) % NBUF, tile_of(base + u + k));
             }
