@@ -564,8 +564,11 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
 #pragma unroll
         for (int t = 0; t < NT; ++t) acc[qb][t] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
     }
-    const half8_t ones = {(_Float16) 1.0f, (_Float16) 1.0f, (_Float16) 1.0f, (_Float16) 1.0f,
-                          (_Float16) 1.0f, (_Float16) 1.0f, (_Float16) 1.0f, (_Float16) 1.0f};
+    half8_t ones = {(_Float16) 1.0f, (_Float16) 1.0f, (_Float16) 1.0f, (_Float16) 1.0f,
+                    (_Float16) 1.0f, (_Float16) 1.0f, (_Float16) 1.0f, (_Float16) 1.0f};
+    // opaque to the compiler, so that it stays in registers instead of being
+    // rebuilt with three moves before every tile's row-sum product
+    asm volatile("" : "+v"(ones));
 
     auto compute = [&](int buf, int T) {
         const bool ring_t = T < n_rt;
