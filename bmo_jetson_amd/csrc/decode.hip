@@ -27,15 +27,23 @@
 // computed.  Keys past the window (and, fused, the slot being written) get
 // weight 0 by select.
 //
-// K side: q (times scale * log2 e) is turned once per wave into 16-bit fixed
-// point per 32-element block, Q_e = round(q_e / sq), |Q_e| <= 30583, and
-// written as four planes of signed base-16 digits, Q_e = sum_i 16^i s_ie with
-// s_ie in [-8, 7], laid out like the code dwords.  The ring keeps K codes as
-// signed nibbles c_e - 8, so v_dot8_i32_i4 gives
-//   sum_e (c_e - 8) Q_e = sum_i 16^i sum_e (c_e - 8) s_ie
-// in 16 instructions per block, exactly, with no correction terms; the block
-// score is that integer times sq times the block scale.  Fixed point costs at
-// most sq / 2 = max|q| / 61166 per query element.
+// K side: q (times scale * log2 e) is turned once per wave into 31-bit fixed
+// point per 32-element block with a power-of-two step: with the block's
+// largest magnitude amax = m * 2^ex (m in [0.5, 1)), sq = 2^(ex-30) and
+// Q_e = rint(q_e / sq), |Q_e| <= 2^30.  Dividing by a power of two is exact,
+// so Q_e sq equals q_e exactly whenever |q_e| >= amax / 64 (an fp32 value of
+// magnitude >= 2^23 is an integer) and is within sq / 2 <= amax * 2^-30 of it
+// otherwise: at least as close as fp32 arithmetic on q itself.  Q_e is
+// written as eight planes of signed base-16 digits, Q_e = sum_i 16^i s_ie
+// with s_ie in [-8, 7], laid out like the code dwords.  The ring keeps K codes
+// as signed nibbles c_e - 8, so v_dot8_i32_i4 gives
+//   sum_e (c_e - 8) Q_e = 2^16 sum_{i>=4} 16^(i-4) P_i + sum_{i<4} 16^i P_i,
+//   P_i = sum_e (c_e - 8) s_ie,
+// in 32 instructions per block, exactly, with no correction terms; the two
+// partial sums stay below 2^24 in magnitude, so each converts to fp32
+// exactly, and the block score is one fma of them with 2^16 sq and sq,
+// rounded once, times the block scale.  A block holding a NaN or an infinity
+// gets sq = NaN, so that head's output is NaN, as fp32 scoring would make it.
 //
 // V side: masking a code dword with 0x000F000F (0x00F000F0) leaves two fp16
 // subnormals equal to c * 2^-24 (c * 2^-20); v_fma_mix_f32 reads them next to
@@ -71,8 +79,11 @@ namespace {
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
-constexpr int kQMax = 30583;      // 7 * (1 + 16 + 256 + 4096): largest |Q|
-constexpr int kQBias = 34952;     // 8 * (1 + 16 + 256 + 4096)
+// Q + kQBias = sum_i 16^i u_i with u_i in [0, 15] and s_i = u_i - 8; any
+// |Q| <= 2^30 lies in the representable [-kQBias, 0x77777777].
+constexpr uint32_t kQBias = 0x88888888u;  // 8 * sum_{i<8} 16^i
+constexpr int kQBits = 30;                // |Q| <= 2^kQBits
+constexpr int kPlanes = 8;                // base-16 digit planes per element
 constexpr float kRescale = 8.0f;  // lazy rescale threshold, log2 units
 // Weights are kept scaled by 2^24 (the running max is stored minus 24), so
 // the fp16-subnormal codes c * 2^-24 multiply them without a per-key scaling.
@@ -132,20 +143,28 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 // K-side scorer: sum_e (c_e - 8) q_e of one block, before the block scale.
 struct Scorer {
-    uint32_t dig[4][4];  // signed digit plane i, laid out like code dword c
-    float sq;            // fixed-point step of this lane's block
+    uint32_t dig[kPlanes][4];  // signed digit plane i, laid out like code dword c
+    float sq;                  // fixed-point step of this lane's block (a power of two)
+    float sqh;                 // 2^16 * sq
 
     // w4: the block's 16 K code bytes as stored (signed nibbles c - 8).
+    // Each partial sum is at most 32 * 8 * 8 * 0x1111 < 2^24 in magnitude.
     __device__ __forceinline__ float operator()(const uint4 &w4) const {
         const int w[4] = {(int) w4.x, (int) w4.y, (int) w4.z, (int) w4.w};
-        int a = 0;
+        int lo = 0, hi = 0;
 #pragma unroll
         for (int i = 3; i >= 0; --i) {
-            if (i != 3) a <<= 4;
+            if (i != 3) {
+                lo <<= 4;
+                hi <<= 4;
+            }
 #pragma unroll
-            for (int c = 0; c < 4; ++c) a = __builtin_amdgcn_sdot8(w[c], (int) dig[i][c], a, false);
+            for (int c = 0; c < 4; ++c) {
+                lo = __builtin_amdgcn_sdot8(w[c], (int) dig[i][c], lo, false);
+                hi = __builtin_amdgcn_sdot8(w[c], (int) dig[i + 4][c], hi, false);
+            }
         }
-        return (float) a * sq;
+        return __builtin_fmaf((float) hi, sqh, (float) lo * sq);
     }
 };
 
@@ -177,9 +196,11 @@ __device__ __forceinline__ void rope_pair(float &a, float &b, float2 cs) {
 }
 
 // One wave turns the query row of its unit into the Scorer digit planes of
-// every block: lane l makes dword c = l % 4 of plane i = (l / 4) % 4 of block
-// (l / 16) % LPK, which holds the digits of elements 4c..4c+3 (low nibbles)
-// and 4c+16..4c+19 (high nibbles).  Results go to this wave's LDS slice.
+// every block: lane l makes dword c = l % 4 of planes i = (l / 4) % 4 and
+// i + 4 of block (l / 16) % LPK, which hold the digits of elements 4c..4c+3
+// (low nibbles) and 4c+16..4c+19 (high nibbles).  Results go to this wave's
+// LDS slice: plane i of block b at dwords b * 32 + i * 4 .. +3, and the
+// block's step at s_sq[b].
 // The query elements lane l works on: 4c..4c+3 and 4c+16..4c+19 of block
 // (l / 16) % LPK, c = l % 4 (loaded early, ahead of the table and quantizer
 // work of the prologue).
@@ -212,23 +233,33 @@ __device__ __forceinline__ void prep_digits(float4 lo, float4 hi, float qscale, 
     const float x[8] = {lo.x * qscale, lo.y * qscale, lo.z * qscale, lo.w * qscale,
                         hi.x * qscale, hi.y * qscale, hi.z * qscale, hi.w * qscale};
     float amax = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) amax = fmaxf(amax, __builtin_fabsf(x[j]));
-    amax = fmaxf(amax, dpp<0xB1>(amax));  // the four lanes c = 0..3 of this block
-    amax = fmaxf(amax, dpp<0x4E>(amax));
-    const float inv = amax > 0.0f ? (float) kQMax / amax : 0.0f;
-    uint32_t dw = 0;
+    float finite = 0.0f;  // 0 when every element is finite, else NaN
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        int Q = (int) __builtin_rintf(x[j] * inv);
-        Q = min(max(Q, -kQMax), kQMax);
-        const uint32_t digit = ((((uint32_t) (Q + kQBias)) >> (4 * i)) & 15u) ^ 8u;
+        amax = fmaxf(amax, __builtin_fabsf(x[j]));
+        finite += x[j] * 0.0f;
+    }
+    amax = fmaxf(amax, dpp<0xB1>(amax));  // the four lanes c = 0..3 of this block
+    amax = fmaxf(amax, dpp<0x4E>(amax));
+    finite += dpp<0xB1>(finite);
+    finite += dpp<0x4E>(finite);
+    // amax = m * 2^ex with m in [0.5, 1): x * 2^(30 - ex) is exact and below
+    // 2^30 in magnitude (0 for amax = 0, whose exponent reads as 0)
+    const int ex = __builtin_amdgcn_frexp_expf(amax);
+    uint32_t dw_lo = 0, dw_hi = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int Q = (int) __builtin_rintf(__builtin_amdgcn_ldexpf(x[j], kQBits - ex));
+        const uint32_t u = (uint32_t) Q + kQBias;  // in [kQBias - 2^30, kQBias + 2^30]
         const int nib = (j < 4) ? 2 * j : 2 * (j - 4) + 1;
-        dw |= digit << (4 * nib);
+        dw_lo |= (((u >> (4 * i)) & 15u) ^ 8u) << (4 * nib);
+        dw_hi |= (((u >> (4 * i + 16)) & 15u) ^ 8u) << (4 * nib);
     }
     if (lane < 16 * LPK) {
-        s_dig[lane] = dw;
-        if ((lane & 15) == 0) s_sq[blk] = amax * (1.0f / (float) kQMax);
+        s_dig[blk * 32 + i * 4 + c] = dw_lo;
+        s_dig[blk * 32 + (i + 4) * 4 + c] = dw_hi;
+        if ((lane & 15) == 0)
+            s_sq[blk] = finite == 0.0f ? __builtin_amdgcn_ldexpf(1.0f, ex - kQBits) : __builtin_nanf("");
     }
 }
 
@@ -274,7 +305,7 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     constexpr int NB = PF + 1;     // resident groups per wave
 
     __shared__ __align__(16) float s_acc[NW * ROWS * D];
-    __shared__ __align__(16) uint32_t s_dig[NW][64];
+    __shared__ __align__(16) uint32_t s_dig[NW][kPlanes * 4 * LPK];
     __shared__ float s_m[NW];
     __shared__ float s_l[NW];
     __shared__ float s_sq[NW][4];
@@ -353,14 +384,15 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     __syncthreads();
     Scorer score;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint4 d4 = *reinterpret_cast<const uint4 *>(&s_dig[wave][blk * 16 + i * 4]);
+    for (int i = 0; i < kPlanes; ++i) {
+        const uint4 d4 = *reinterpret_cast<const uint4 *>(&s_dig[wave][blk * 32 + i * 4]);
         score.dig[i][0] = d4.x;
         score.dig[i][1] = d4.y;
         score.dig[i][2] = d4.z;
         score.dig[i][3] = d4.w;
     }
     score.sq = s_sq[wave][blk];
+    score.sqh = score.sq * 65536.0f;
 
     // Softmax state of this lane's keys (log2 domain): mm = running max - 24,
     // mt = running max + 8 (the lazy rescale threshold), l = sum of weights
