@@ -19,7 +19,8 @@ synchronizations, timed by a HIP event pair on the replay stream.  The
 roofline entry divides one launch's algorithmic bytes by the mean launch
 duration from that region (step time / 32, kernel gaps included).
 
-Also reported: B=1 latency (one layer, 32 heads, W=512,
+Also reported: BASELINE config 4 (256 sessions, fused append + decode, timed
+the same way, with its own roofline entry), B=1 latency (one layer, 32 heads, W=512,
 write head at position 700; fused append+decode as the reference kernel does,
 and decode alone), the depformer frame, and the CPU
 baseline (the oracle's fp32 restatement of the reference CPU path, timed on
@@ -100,8 +101,11 @@ def capture_graph(torch, launch):
 
 
 def time_steps(torch, launch_layer, n_layers, steps, warmup):
-    """Runs `warmup` eager steps, captures one step (n_layers launches, one
-    per layer, as the model runs them) into a HIP graph, and times exactly
+    """Runs one eager step, captures one step (n_layers launches, one per
+    layer, as the model runs them) into a HIP graph, replays it `warmup` times
+    (the untimed warmup steps, right before the timed region, so that the GPU
+    enters it at its working clocks: after the idle spell of the graph capture
+    the first milliseconds of work ran about 2% slower), and times exactly
     `steps` replays between two torch.cuda.synchronize() calls with a HIP
     event pair recorded on the replay stream.  Returns ms per step; the mean
     launch duration is that over n_layers (it includes the small gaps between
@@ -109,9 +113,8 @@ def time_steps(torch, launch_layer, n_layers, steps, warmup):
     `steps` more replays, each between its own event pair, give the per-step
     distribution (median, min, max), outside the timed region."""
     stream = torch.cuda.current_stream()
-    for _ in range(warmup):
-        for layer in range(n_layers):
-            launch_layer(layer, stream)
+    for layer in range(n_layers):
+        launch_layer(layer, stream)
     torch.cuda.synchronize()
 
     def whole_step(st):
@@ -119,8 +122,8 @@ def time_steps(torch, launch_layer, n_layers, steps, warmup):
             launch_layer(layer, st)
 
     graph = capture_graph(torch, whole_step)
-    graph.replay()
-    torch.cuda.synchronize()
+    for _ in range(max(1, warmup)):
+        graph.replay()
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -339,6 +342,83 @@ def bench_gemv(torch, reps=50):
     return res
 
 
+def run_decode(torch, config, steps, warmup, sessions=None):
+    """BASELINE config 3 (decode) or 4 (fused append + decode) through 32
+    layers: fills the ring, times `steps` graph-replayed steps after `warmup`
+    (time_steps) and returns the figures together with the live ring and the
+    inputs (for the CPU baseline)."""
+    from bmo_jetson_amd import KVRing
+
+    H, D, W, L = 32, 128, 512, 32
+    S = sessions or (64 if config == "cfg3" else 256)
+    fused = config == "cfg4"
+    seed = 0xB0A00003 if config == "cfg3" else 0xB0A00004
+    rng = np.random.default_rng(seed)
+    pos_host = rng.integers(512, 4096, size=S).astype(np.int64)
+    log(f"[bench] {config}: S={S} L={L} H={H} D={D} W={W} fused={fused}; filling ring")
+    t_fill = time.time()
+    ring = KVRing(L, S, H, D, W)
+    # cfg4 appends the token at pos, so the ring holds the window before it
+    fill_ring(torch, ring, L, S, H, D, W, pos_host - (1 if fused else 0), seed)
+    log(f"[bench] ring {ring.nbytes / 1e9:.2f} GB filled in {time.time() - t_fill:.1f} s")
+
+    pos = torch.tensor(pos_host, dtype=torch.int32, device="cuda")
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed + 7)
+    q = torch.randn((L, S, H, D), device="cuda", generator=g)
+    out = torch.empty((L, S, H, D), device="cuda")
+    if fused:
+        kn = torch.randn((L, S, H, D), device="cuda", generator=g)
+        vn = torch.randn((L, S, H, D), device="cuda", generator=g)
+
+    def launch_layer(layer, st):
+        if fused:
+            ring.append_decode(layer, pos, q[layer], kn[layer], vn[layer], out[layer], H, stream=st)
+        else:
+            ring.decode(layer, pos, q[layer], out[layer], H, stream=st)
+
+    ms_per_step, per_step = time_steps(torch, launch_layer, L, steps, warmup)
+    launch_ms = ms_per_step / L
+    per_step_bytes = unit_bytes(H, D, W) * S * L
+    if fused:
+        per_step_bytes += fused_extra_bytes(H, D) * S * L
+    value = per_step_bytes / (ms_per_step * 1e-3) / 1e9
+    launch_bytes = per_step_bytes // L
+    achieved = launch_bytes / (launch_ms * 1e-3) / 1e9
+    log(f"[bench] {config}: {ms_per_step:.3f} ms/step, {value:.1f} GB/s; per launch "
+        f"{launch_ms * 1e3:.2f} us -> {achieved:.1f} GB/s")
+    return {
+        "H": H, "D": D, "W": W, "L": L, "S": S,
+        "ring": ring, "pos_host": pos_host, "q": q, "out": out,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "ms_per_step": round(ms_per_step, 4),
+        "step_ms_dist": {"median": round(float(np.median(per_step)), 4),
+                         "min": round(min(per_step), 4), "max": round(max(per_step), 4),
+                         "n": len(per_step), "note": "separate replays after the timed region"},
+        "hbm_frac": round(value / HBM_PEAK_GBS, 4),
+        "config": {
+            "workload": (f"{config}: Q4_0 ring {'fused append+' if fused else ''}decode "
+                         f"attention, S={S} sessions x L={L} layers, H={H} x D={D}, W={W}, "
+                         f"pos~U[512,4096), 1% x8 outliers"),
+            "sessions": S, "layers": L, "heads": H, "head_dim": D, "window": W,
+            "bytes_per_step": per_step_bytes, "launches_per_step": L,
+            "parallelism": "none (1 GPU; sessions would shard across GPUs)",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": read_traffic(config),
+            "kernel": "decode_kernel<128, 1, 2, %s>" % ("true" if fused else "false"),
+            "launch_us": round(launch_ms * 1e3, 3),
+            "bytes_per_launch": launch_bytes,
+        },
+    }
+
+
 def cpu_baseline(torch, ring, L, S, H, D, W, pos_host, q_dev, out_dev, budget_s):
     """Times the oracle's fp32 restatement of the reference CPU path
     (src/bmo_compute.cpp:927-970) on host threads over a sample of the same
@@ -389,9 +469,6 @@ def cpu_baseline(torch, ring, L, S, H, D, W, pos_host, q_dev, out_dev, budget_s)
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    # >= 100 timed steps after >= 20 warmups (at 20 steps the timed region's
-    # mean step was 1.4% above the median of individually timed replays: a
-    # fixed start-up cost spread over few steps)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="cfg3", choices=["cfg3", "cfg4"])
@@ -399,6 +476,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-b1", action="store_true")
+    ap.add_argument("--no-cfg4", action="store_true",
+                    help="skip the BASELINE config 4 leg (fused append + decode, 256 sessions)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only run the cfg5 chunked-prefill leg and print its JSON (profiling)")
     ap.add_argument("--gemv-only", action="store_true",
@@ -436,87 +515,36 @@ def main():
         print(json.dumps({"gemv": bench_gemv(torch)}), flush=True)
         return
 
-    from bmo_jetson_amd import KVRing
-
-    H, D, W, L = 32, 128, 512, 32
-    S = args.sessions or (64 if args.config == "cfg3" else 256)
-    fused = args.config == "cfg4"
-    seed = 0xB0A00003 if args.config == "cfg3" else 0xB0A00004
-    rng = np.random.default_rng(seed)
-    pos_host = rng.integers(512, 4096, size=S).astype(np.int64)
-    log(f"[bench] {args.config}: S={S} L={L} H={H} D={D} W={W} fused={fused}; filling ring")
-    t_fill = time.time()
-    ring = KVRing(L, S, H, D, W)
-    # cfg4 appends the token at pos, so the ring holds the window before it
-    fill_ring(torch, ring, L, S, H, D, W, pos_host - (1 if fused else 0), seed)
-    log(f"[bench] ring {ring.nbytes / 1e9:.2f} GB filled in {time.time() - t_fill:.1f} s")
-
-    stream = torch.cuda.current_stream()
-    pos = torch.tensor(pos_host, dtype=torch.int32, device="cuda")
-    g = torch.Generator(device="cuda")
-    g.manual_seed(seed + 7)
-    q = torch.randn((L, S, H, D), device="cuda", generator=g)
-    out = torch.empty((L, S, H, D), device="cuda")
-    if fused:
-        kn = torch.randn((L, S, H, D), device="cuda", generator=g)
-        vn = torch.randn((L, S, H, D), device="cuda", generator=g)
-
-    def launch_layer(layer, st):
-        if fused:
-            ring.append_decode(layer, pos, q[layer], kn[layer], vn[layer], out[layer], H, stream=st)
-        else:
-            ring.decode(layer, pos, q[layer], out[layer], H, stream=st)
-
-    ms_per_step, per_step = time_steps(torch, launch_layer, L, args.steps, args.warmup)
-    launch_ms = ms_per_step / L
-    per_step_bytes = unit_bytes(H, D, W) * S * L
-    if fused:
-        per_step_bytes += fused_extra_bytes(H, D) * S * L
-    value = per_step_bytes / (ms_per_step * 1e-3) / 1e9
-    launch_bytes = per_step_bytes // L
-    achieved = launch_bytes / (launch_ms * 1e-3) / 1e9
-    log(f"[bench] {ms_per_step:.3f} ms/step, {value:.1f} GB/s; per launch "
-        f"{launch_ms * 1e3:.2f} us -> {achieved:.1f} GB/s")
-    kernel = "decode_kernel<128, 1, 2, %s>" % ("true" if fused else "false")
-    traffic = read_traffic(args.config)
-
+    run = run_decode(torch, args.config, args.steps, args.warmup, args.sessions)
+    H, D, W, L, S = run["H"], run["D"], run["W"], run["L"], run["S"]
     result = {
         "metric": METRIC,
-        "value": round(value, 2),
+        "value": run["value"],
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4),
-        "step_ms_dist": {"median": round(float(np.median(per_step)), 4),
-                         "min": round(min(per_step), 4), "max": round(max(per_step), 4),
-                         "n": len(per_step), "note": "separate replays after the timed region"},
+        "ms_per_step": run["ms_per_step"],
+        "step_ms_dist": run["step_ms_dist"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {
-            "workload": (f"{args.config}: Q4_0 ring {'fused append+' if fused else ''}decode "
-                         f"attention, S={S} sessions x L={L} layers, H={H} x D={D}, W={W}, "
-                         f"pos~U[512,4096), 1% x8 outliers"),
-            "sessions": S, "layers": L, "heads": H, "head_dim": D, "window": W,
-            "bytes_per_step": per_step_bytes, "launches_per_step": L,
-            "parallelism": "none (1 GPU; sessions would shard across GPUs)",
-        },
-        "hbm_frac": round(value / HBM_PEAK_GBS, 4),
-        "roofline": {
-            "bound": "hbm",
-            "achieved": round(achieved, 2),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": traffic,
-            "kernel": kernel,
-            "launch_us": round(launch_ms * 1e3, 3),
-            "bytes_per_launch": launch_bytes,
-        },
+        "config": run["config"],
+        "hbm_frac": run["hbm_frac"],
+        "roofline": run["roofline"],
     }
+    if args.config == "cfg3" and not args.no_cfg4:
+        # BASELINE config 4 (fused append + decode, 256 sessions) at the same
+        # step count; its 19.3 GB ring is freed before the other legs
+        c4 = run_decode(torch, "cfg4", args.steps, args.warmup, None)
+        c4["ring"].close()
+        result["cfg4"] = {k: c4[k] for k in ("value", "unit", "ms_per_step", "step_ms_dist",
+                                             "hbm_frac", "roofline", "config")}
+        del c4
+        torch.cuda.empty_cache()
+    ring, pos_host, q, out = run["ring"], run["pos_host"], run["q"], run["out"]
 
     if not args.no_b1:
         result["b1"] = bench_b1(torch)

@@ -321,29 +321,22 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     const int h = unit - b * p.n_heads;
 
     const RingGeom &g = p.g;
-    const int sid = p.session_ids ? p.session_ids[b] : b;
-    const int pos = p.pos ? p.pos[b] : p.pos_scalar;
-    float *out_row = p.out + (int64_t) unit * D;
-    if (sid < 0 || sid >= g.n_sessions || pos < 0) {
-        for (int i = threadIdx.x; i < D; i += blockDim.x) out_row[i] = 0.0f;
-        return;
-    }
+    const int sid_in = p.session_ids ? p.session_ids[b] : b;
+    const bool sid_ok = sid_in >= 0 && sid_in < g.n_sessions;
+    const int sid = sid_ok ? sid_in : 0;  // an in-bounds stripe for loads issued before the check
     const int q_per_kv = p.n_heads / p.n_kv;
     const int kvh = h / q_per_kv;
-    const int window = (int) min((int64_t) pos + 1, (int64_t) g.n_ctx);
-    const int cur = pos % g.n_ctx;
     uint8_t *stripe = p.base + g.stripe_offset(p.layer, sid, kvh);
+    float *out_row = p.out + (int64_t) unit * D;
 
     // Contiguous group run of this wave.  Fused with several waves per
     // unit, wave 0 quantizes and attends to the current token and the other
     // waves split the window, so the new token's work is off the window's
     // critical path.
-    const int n_grp = (window + G - 1) / G;
     constexpr bool kSplitNew = FUSED && NW > 1;
     constexpr int NWW = kSplitNew ? NW - 1 : NW;  // waves that stream the window
     const int ww = kSplitNew ? wave - 1 : wave;
-    const int g0 = ww < 0 ? 0 : ww * n_grp / NWW;
-    const int n_it = ww < 0 ? 0 : (ww + 1) * n_grp / NWW - g0;
+    int g0 = 0, n_it = 0;
 
     struct Grp {
         uint4 k, v;
@@ -365,11 +358,30 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     // on every path and the compiler's wait counts stay exact.
     auto load_clamped = [&](int it, Grp &T) { load(min(it, g.n_groups - 1 - g0), T); };
     Grp buf[NB];
-#pragma unroll
-    for (int j = 0; j < NB - 1; ++j) load_clamped(j, buf[j]);
-
     float4 q_lo, q_hi;
-    prep_load<D>(p.q + (int64_t) unit * D, lane, q_lo, q_hi);
+    // With one wave per unit the run starts at group 0 whatever the
+    // position, so the first groups and the query are requested before the
+    // position is read (the scalar read's latency then overlaps theirs).
+    if constexpr (NW == 1) {
+#pragma unroll
+        for (int j = 0; j < NB - 1; ++j) load_clamped(j, buf[j]);
+        prep_load<D>(p.q + (int64_t) unit * D, lane, q_lo, q_hi);
+    }
+    const int pos = p.pos ? p.pos[b] : p.pos_scalar;
+    if (!sid_ok || pos < 0) {
+        for (int i = threadIdx.x; i < D; i += blockDim.x) out_row[i] = 0.0f;
+        return;
+    }
+    const int window = (int) min((int64_t) pos + 1, (int64_t) g.n_ctx);
+    const int cur = pos % g.n_ctx;
+    const int n_grp = (window + G - 1) / G;
+    g0 = ww < 0 ? 0 : ww * n_grp / NWW;
+    n_it = ww < 0 ? 0 : (ww + 1) * n_grp / NWW - g0;
+    if constexpr (NW > 1) {
+#pragma unroll
+        for (int j = 0; j < NB - 1; ++j) load_clamped(j, buf[j]);
+        prep_load<D>(p.q + (int64_t) unit * D, lane, q_lo, q_hi);
+    }
     // Fused: wave 0's lane blk (kk == 0) holds K block blk of the current
     // token, lane LPK + blk (kk == 1) its V block; loaded here so that their
     // latency overlaps the query's.
@@ -494,22 +506,16 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
         }
     }
 
-    // Bring every lane to the wave max, undo the 2^-20 scale of elements
-    // 16..31, fold the -8 code offset, and sum the lanes of each row that
-    // share a block.
+    // Bring every lane to the wave max (the factor is folded into one fma
+    // per element), undo the 2^-20 scale of elements 16..31, fold the -8
+    // code offset, and sum the lanes of each row that share a block.
     const float m_wave = wave_max(mm);
-    {
-        const float f = __builtin_amdgcn_exp2f(mm - m_wave);
-        l *= f;
-        csum *= f;
+    const float f = __builtin_amdgcn_exp2f(mm - m_wave);
+    const float l_wave = wave_sum(l * f) * (1.0f / LPK);
+    const float c8 = (-8.0f / 16777216.0f) * (csum * f);  // -8 * sum of p * d, in acc units
+    const float f_hi = f * 0.0625f;
 #pragma unroll
-        for (int e = 0; e < 32; ++e) acc[e] *= f;
-    }
-    const float l_wave = wave_sum(l) * (1.0f / LPK);
-    const float c8 = -8.0f / 16777216.0f * csum;  // -8 * sum of p * d, in acc units
-#pragma unroll
-    for (int e = 0; e < 32; ++e)
-        acc[e] = row_block_sum<LPK>(e < 16 ? acc[e] + c8 : __builtin_fmaf(acc[e], 0.0625f, c8));
+    for (int e = 0; e < 32; ++e) acc[e] = row_block_sum<LPK>(__builtin_fmaf(acc[e], e < 16 ? f : f_hi, c8));
     // l_wave is 2^24 times the weight sum: the output divides by it times 2^-24
     const int row = lane >> 4;
     if ((lane & 15) < LPK) {
@@ -518,22 +524,29 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
         for (int c = 0; c < 8; ++c)
             dst[c] = make_float4(acc[4 * c], acc[4 * c + 1], acc[4 * c + 2], acc[4 * c + 3]);
     }
-    if (lane == 0) {
-        s_m[wave] = m_wave;
-        s_l[wave] = l_wave;
+    if constexpr (NW > 1) {
+        if (lane == 0) {
+            s_m[wave] = m_wave;
+            s_l[wave] = l_wave;
+        }
     }
     __syncthreads();
 
     // Merge waves and rows; a workgroup may have fewer threads than head_dim.
-    float M = s_m[0];
-#pragma unroll
-    for (int w = 1; w < NW; ++w) M = fmaxf(M, s_m[w]);
     float fw[NW];
-    float L = 0.0f;  // sum of weights of the whole window
+    float L = l_wave;  // sum of weights of the whole window
+    if constexpr (NW > 1) {
+        float M = s_m[0];
 #pragma unroll
-    for (int w = 0; w < NW; ++w) {
-        fw[w] = __builtin_amdgcn_exp2f(s_m[w] - M);
-        L = __builtin_fmaf(fw[w], s_l[w], L);
+        for (int w = 1; w < NW; ++w) M = fmaxf(M, s_m[w]);
+        L = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            fw[w] = __builtin_amdgcn_exp2f(s_m[w] - M);
+            L = __builtin_fmaf(fw[w], s_l[w], L);
+        }
+    } else {
+        fw[0] = 1.0f;
     }
     // Thread t sums the rows of waves w = t / D (mod the number of row
     // groups) for output t % D; row groups beyond the first add through LDS.

@@ -42,3 +42,9 @@ def test_bench_json_line(gpu, monkeypatch, capsys):
     # value is the whole step's bytes over its time; achieved is one launch's
     assert abs(r["value"] - r["config"]["bytes_per_step"] / (r["ms_per_step"] * 1e-3) / 1e9) \
         < 1e-3 * r["value"] + 0.01
+    # BASELINE config 4 leg: fused append + decode over 256 sessions
+    c4 = r["cfg4"]
+    assert c4["config"]["workload"].startswith("cfg4") and c4["config"]["sessions"] == 256
+    assert c4["value"] > 0 and c4["roofline"]["kernel"].endswith("true>")
+    assert abs(c4["value"] - c4["config"]["bytes_per_step"] / (c4["ms_per_step"] * 1e-3) / 1e9) \
+        < 1e-3 * c4["value"] + 0.01
