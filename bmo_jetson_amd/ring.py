@@ -63,6 +63,9 @@ class KVRing:
             err = L.bmo_kv_ring_last_error(None)
             raise RuntimeError(f"bmo_kv_ring_create failed: {err.decode() if err else 'unknown'}")
         self._h = h
+        # bound here so that __del__ never needs module globals, which the
+        # interpreter may already have cleared when it runs at exit
+        self._free = L.bmo_kv_ring_free
         self.n_layers = n_layers
         self.n_sessions = n_sessions
         self.n_kv_heads = n_kv_heads
@@ -71,12 +74,16 @@ class KVRing:
 
     # -- lifetime ---------------------------------------------------------------
     def close(self) -> None:
-        if getattr(self, "_h", None):
-            lib().bmo_kv_ring_free(self._h)
+        h = getattr(self, "_h", None)
+        if h:
             self._h = None
+            self._free(h)
 
     def __del__(self):
-        self.close()
+        try:
+            self.close()
+        except Exception:  # interpreter teardown: nothing left to report to
+            pass
 
     def __enter__(self):
         return self

@@ -98,11 +98,101 @@ def test_error_bounds():
                   .repeat(32, 1)[clamped])
 
 
-def test_planted_mistake_is_caught():
-    """A quantizer with the wrong tie rule (last occurrence wins) must fail the
-    tie KATs: the KATs are sensitive to this class of slip."""
-    x = np.array(KAT["cases"][3]["x"], np.float32)
-    amax = np.max(np.abs(x))
-    last = np.where(np.abs(x) == amax)[0][-1]
-    d_wrong = np.float32(x[last] / np.float32(-8.0)).astype(np.float16).view(np.uint16)
-    assert int(d_wrong) != KAT["cases"][3]["d"]
+# ---- the checks above must catch plausible slips -----------------------------
+#
+# quantize_numpy is a vectorized restatement of the same published steps with
+# switches for the slips a restatement could make.  With no switch set it
+# must pass every check; each mutant must fail at least one.  The checks are
+# functions of the quantizer, so they are exactly the ones the oracle passes.
+
+def quantize_numpy(x, tie_last=False, divisor=-8.0, fused=False, swap_nibbles=False,
+                   clamp=True, id_from_fp16=False, round_even=False):
+    """x: (n, 32) float32 -> (d bits uint16 [n], qs uint8 [n, 16])."""
+    x = np.ascontiguousarray(x, np.float32)
+    n = x.shape[0]
+    ax = np.abs(x)
+    idx = 31 - np.argmax(ax[:, ::-1], axis=1) if tie_last else np.argmax(ax, axis=1)
+    m = x[np.arange(n), idx]
+    d = (m / np.float32(divisor)).astype(np.float32)
+    d16 = d.astype(np.float16)
+    dd = d16.astype(np.float32) if id_from_fp16 else d
+    with np.errstate(divide="ignore"):
+        idv = np.where(dd != 0, (np.float32(1.0) / dd).astype(np.float32), np.float32(0.0))
+    if round_even:
+        q = np.rint((x * idv[:, None]).astype(np.float32)).astype(np.int64) + 8
+    elif fused:
+        q = np.trunc(x.astype(np.float64) * idv[:, None].astype(np.float64) + 8.5).astype(np.int64)
+    else:
+        t = (x * idv[:, None]).astype(np.float32)
+        q = np.trunc((t + np.float32(8.5)).astype(np.float32)).astype(np.int64)
+    if clamp:
+        q = np.minimum(q, 15)
+    lo, hi = q[:, :16], q[:, 16:]
+    qs = (hi | (lo << 4)) if swap_nibbles else (lo | (hi << 4))
+    return d16.view(np.uint16), (qs & 0xFF).astype(np.uint8)
+
+
+def _oracle_quant(x):
+    b = oracle.quantize_q4_0(x)
+    return b["d"].copy(), b["qs"].copy()
+
+
+def check_kats(quant):
+    for c in KAT["cases"]:
+        d, qs = quant(np.array(c["x"], np.float32).reshape(1, 32))
+        if int(d[0]) != c["d"] or [int(v) for v in qs[0]] != c["qs"]:
+            return False
+    return True
+
+
+def check_brute_force(quant):
+    x = _blocks_random(11, 4000, outlier_p=0.01)
+    d, qs = quant(x)
+    qs = qs.astype(np.int32)
+    codes = np.concatenate([qs & 0xF, qs >> 4], axis=-1)
+    amax_idx = np.argmax(np.abs(x), axis=1)
+    m = x[np.arange(len(x)), amax_idx]
+    dm = (m / np.float32(-8.0)).astype(np.float32)
+    t = (x * (np.float32(1.0) / dm).astype(np.float32)[:, None]).astype(np.float32)
+    cand = np.arange(16, dtype=np.float64)[None, None, :] - 8.0
+    dist = np.abs(cand - t.astype(np.float64)[..., None])
+    best = np.argmin(dist + 1e-12 * (15 - np.arange(16))[None, None, :], axis=-1)
+    return bool(np.array_equal(codes, best) and np.all(codes[np.arange(len(x)), amax_idx] == 0))
+
+
+def check_scale(quant):
+    x = _blocks_random(12, 2000)
+    d, _ = quant(x)
+    m = x[np.arange(len(x)), np.argmax(np.abs(x), axis=1)]
+    ref = (m / np.float32(-8.0)).astype(np.float32).astype(np.float16).view(np.uint16)
+    return bool(np.array_equal(d, ref))
+
+
+CHECKS = (check_kats, check_brute_force, check_scale)
+
+
+def test_checks_pass_oracle_and_numpy_restatement():
+    for check in CHECKS:
+        assert check(_oracle_quant), check.__name__
+        assert check(quantize_numpy), check.__name__
+
+
+MUTANTS = {
+    "tie_last": dict(tie_last=True),            # >= in the max scan: last occurrence wins
+    "divisor_plus_8": dict(divisor=8.0),        # sign of d flipped
+    "divisor_minus_7": dict(divisor=-7.0),      # a symmetric 7-level scale
+    "swap_nibbles": dict(swap_nibbles=True),    # element j in the high nibble
+    "no_clamp": dict(clamp=False),              # min(15, .) dropped
+    "id_from_fp16": dict(id_from_fp16=True),    # 1/d taken from the rounded scale
+    "round_even": dict(round_even=True),        # rint instead of trunc(x*id + 8.5)
+    "fused": dict(fused=True),                  # x*id + 8.5 contracted into one rounding
+}
+
+
+@pytest.mark.parametrize("name", sorted(MUTANTS))
+def test_planted_mistake_is_caught(name):
+    """Each plausible slip in a restatement of the quantizer fails at least one
+    of the checks the oracle passes."""
+    quant = lambda x: quantize_numpy(x, **MUTANTS[name])
+    failed = [c.__name__ for c in CHECKS if not c(quant)]
+    assert failed, f"mutant {name} passes every check"
