@@ -14,6 +14,7 @@ from ._lib import LIB_PATH, lib, header_symbols, build  # noqa: F401
 from .ring import (  # noqa: F401
     KVRing,
     RingError,
+    Session,
     launch_decode_attention,
     positions_advance,
     gemv_q4_0_q8_1,
@@ -24,6 +25,7 @@ from .ring import (  # noqa: F401
 __all__ = [
     "KVRing",
     "RingError",
+    "Session",
     "launch_decode_attention",
     "positions_advance",
     "gemv_q4_0_q8_1",

@@ -41,6 +41,16 @@ SIGNATURES = {
     "bmo_kv_ring_export_q4_0": (i64, [P, i32, i32, i32, i32, i32, P, i64]),
     "bmo_kv_ring_import_q4_0": (i64, [P, i32, i32, i32, i32, i32, P, i64]),
     "bmo_launch_decode_attention": (None, [P, P, P, P, P, P, i32, i32, i32, i32, i32, i32, P, P]),
+    "bmo_attn_session_create": (P, [P, i32, i32, f32, f32]),
+    "bmo_attn_session_free": (None, [P]),
+    "bmo_attn_session_reset": (i32, [P]),
+    "bmo_attn_session_pos": (i64, [P]),
+    "bmo_attn_session_stream": (P, [P]),
+    "bmo_attn_session_forward": (i32, [P, i32, P, P, P, P]),
+    "bmo_attn_session_capture": (i32, [P, P, P, P, P]),
+    "bmo_attn_session_has_graph": (i32, [P]),
+    "bmo_attn_session_replay": (i32, [P, i32]),
+    "bmo_attn_session_last_error": (ctypes.c_char_p, [P]),
 }
 
 

@@ -87,6 +87,16 @@ __global__ __launch_bounds__(256) void advance_kernel(int *pos, int n, int delta
     if (i < n) pos[i] += delta;
 }
 
+// pos[0] = value (a session handle's device position; a kernel rather than a
+// copy, so that no host buffer has to outlive the call).
+__global__ __launch_bounds__(64) void set_pos_kernel(int *pos, int value) {
+    if (threadIdx.x == 0) pos[0] = value;
+}
+
+void launch_set_pos(int *pos, int value, hipStream_t stream) {
+    hipLaunchKernelGGL(set_pos_kernel, dim3(1), dim3(64), 0, stream, pos, value);
+}
+
 void launch_advance(int *pos, int n, int delta, hipStream_t stream) {
     hipLaunchKernelGGL(advance_kernel, dim3((unsigned) ((n + 255) / 256)), dim3(256), 0, stream, pos, n,
                        delta);

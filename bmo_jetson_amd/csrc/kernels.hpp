@@ -71,6 +71,7 @@ struct PrefillParams {
 // hipGetLastError().  launch_decode returns false for an unsupported head_dim.
 void launch_append(const AppendParams &p, hipStream_t stream);
 void launch_advance(int *pos, int n, int delta, hipStream_t stream);
+void launch_set_pos(int *pos, int value, hipStream_t stream);
 bool launch_decode(const DecodeParams &p, bool fused, hipStream_t stream);
 // stage, attend, commit (three kernels in stream order); false for an
 // unsupported head_dim.

@@ -227,6 +227,85 @@ class KVRing:
             raise RuntimeError(f"bmo_kv_ring_import_q4_0 failed with code {rc}")
 
 
+class Session:
+    """Per-session handle (bmo_attn_session_*): one session of a ring with its
+    own HIP stream and device position; ``forward`` runs one token's fused
+    append + attention through every layer at a position and advances it,
+    ``capture`` / ``replay`` do the same from a HIP graph recorded in the
+    library.  q/out are [n_layers][n_heads][head_dim] and k/v
+    [n_layers][n_kv_heads][head_dim] fp32 device buffers."""
+
+    def __init__(self, ring: KVRing, session: int, n_heads: int, scale: float = 0.0,
+                 rope_theta: float = 0.0):
+        L = lib()
+        h = L.bmo_attn_session_create(ring.handle, session, n_heads, float(scale),
+                                      float(rope_theta))
+        if not h:
+            err = L.bmo_attn_session_last_error(None)
+            raise RuntimeError(f"bmo_attn_session_create failed: {err.decode() if err else 'unknown'}")
+        self._h = h
+        self._free = L.bmo_attn_session_free
+        self.ring = ring  # the ring must outlive the handle
+        self.session = session
+        self.n_heads = n_heads
+
+    def close(self) -> None:
+        h = getattr(self, "_h", None)
+        if h:
+            self._h = None
+            self._free(h)
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # interpreter teardown
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    @property
+    def handle(self) -> int:
+        return self._h
+
+    def last_error(self) -> str | None:
+        e = lib().bmo_attn_session_last_error(self._h)
+        return e.decode() if e else None
+
+    def _check(self, fn: str, rc: int) -> None:
+        if rc != 0:
+            raise RingError(fn, rc, self.last_error())
+
+    @property
+    def pos(self) -> int:
+        return int(lib().bmo_attn_session_pos(self._h))
+
+    @property
+    def stream(self) -> int:
+        return int(lib().bmo_attn_session_stream(self._h) or 0)
+
+    def reset(self) -> None:
+        self._check("bmo_attn_session_reset", lib().bmo_attn_session_reset(self._h))
+
+    def forward(self, pos: int, q, k, v, out) -> None:
+        self._check("bmo_attn_session_forward", lib().bmo_attn_session_forward(
+            self._h, int(pos), _ptr(q), _ptr(k), _ptr(v), _ptr(out)))
+
+    def capture(self, q, k, v, out) -> None:
+        self._check("bmo_attn_session_capture", lib().bmo_attn_session_capture(
+            self._h, _ptr(q), _ptr(k), _ptr(v), _ptr(out)))
+
+    @property
+    def has_graph(self) -> bool:
+        return bool(lib().bmo_attn_session_has_graph(self._h))
+
+    def replay(self, pos: int) -> None:
+        self._check("bmo_attn_session_replay", lib().bmo_attn_session_replay(self._h, int(pos)))
+
+
 def launch_decode_attention(q, k, v, k_cache, v_cache, out, head_dim: int, n_heads: int,
                             n_kv_heads: int, n_ctx: int, n_past: int, layer: int, stream=None,
                             pos_dev=None) -> None:

@@ -17,9 +17,10 @@
  *   - Every call is asynchronous on its stream unless it says otherwise.  A
  *     call that writes slots (append, fused append+decode, write, reset,
  *     import) must be ordered with the calls that read those slots, as on one
- *     stream; decode calls alone may overlap.  Only bmo_kv_ring_create and
- *     bmo_kv_ring_prefill (its staging buffer, when a staged call needs a
- *     larger one than the ring holds) allocate device memory.
+ *     stream; decode calls alone may overlap.  Only bmo_kv_ring_create,
+ *     bmo_attn_session_create and bmo_kv_ring_prefill (its staging buffer,
+ *     when a staged call needs a larger one than the ring holds) allocate
+ *     device memory.
  *   - Functions returning int return BMO_ATTN_OK (0) or an error code below;
  *     bmo_kv_ring_last_error() then describes the most recent failure on that
  *     ring (as bmo_last_error does per handle, src/bmo_api.h:145).
@@ -121,7 +122,10 @@ BMO_ATTN_API const char *bmo_kv_ring_last_error(const bmo_kv_ring_t *ring);
  * can be replayed with new positions (the role of pos_dev in
  * src/bmo_api.cpp:168-171).  An entry whose session id or position is out of
  * range is skipped: nothing is written to the ring and its output rows are
- * set to zero.
+ * set to zero.  The entries of one call that writes slots (append, fused
+ * append + decode, with or without RoPE) must name distinct sessions: one
+ * entry's write of slot pos % n_ctx would race with another entry of the same
+ * session reading that slot in its window.
  *   q, out:        [n_batch][n_heads][head_dim] fp32 (q after RoPE)
  *   k_new, v_new:  [n_batch][n_kv_heads][head_dim] fp32
  *   scale:         softmax scale; <= 0 selects 1/sqrt(head_dim)
@@ -253,6 +257,80 @@ BMO_ATTN_API int64_t bmo_kv_ring_import_q4_0(bmo_kv_ring_t *ring, int layer,
  * when a staged call needs a larger staging buffer than the ring holds; call
  * it once eagerly before capturing it. */
 BMO_ATTN_API int bmo_positions_advance(int *pos_dev, int n, int delta, void *stream);
+
+/* ---- per-session handle ------------------------------------------------------ */
+/*
+ * The attention part of the reference's bmo_handle (src/bmo_api.cpp:164-172):
+ * one session of a ring, a HIP stream of its own (non-blocking, default
+ * priority), a device-resident position that every launch reads (the
+ * reference's pos_dev), and a mutex that serializes the handle's calls
+ * (src/bmo_api.cpp:28, :415).  A token step runs the fused append +
+ * attention of every layer of the ring at one position (with RoPE when
+ * rope_theta > 0) and advances the position, as bmo_forward_temporal2 does
+ * with h->pos = pos + 1 (src/bmo_api.cpp:501).  For a step:
+ *   q, out:  [n_layers][n_heads][head_dim] fp32, device
+ *   k, v:    [n_layers][n_kv_heads][head_dim] fp32, device
+ * The ring must outlive its handles; one handle per ring session (two handles
+ * on one session race on its slots).  Handles on distinct sessions of one
+ * ring may run concurrently.  Functions returning int return BMO_ATTN_OK or
+ * an error code; bmo_attn_session_last_error() gives the message.
+ */
+typedef struct bmo_attn_session bmo_attn_session_t;
+
+/* Creates a handle for `session` of `ring` with n_heads query heads (a
+ * multiple of the ring's n_kv_heads), softmax scale (<= 0: 1/sqrt(head_dim))
+ * and rope_theta (0: q and k arrive with RoPE applied).  The position starts
+ * at 0; the ring is not cleared.  Returns NULL on failure;
+ * bmo_attn_session_last_error(NULL) then gives the calling thread's reason
+ * (the reference prints init failures to stderr, src/bmo_api.cpp:196-205;
+ * this does both). */
+BMO_ATTN_API bmo_attn_session_t *bmo_attn_session_create(bmo_kv_ring_t *ring, int session,
+                                                         int n_heads, float scale,
+                                                         float rope_theta);
+
+/* Waits for the handle's work and releases it.  NULL-safe. */
+BMO_ATTN_API void bmo_attn_session_free(bmo_attn_session_t *s);
+
+/* Position 0 and the session's K/V zeroed in every layer; synchronous (the
+ * K/V part of bmo_reset, src/bmo_api.cpp:258-272). */
+BMO_ATTN_API int bmo_attn_session_reset(bmo_attn_session_t *s);
+
+/* The next position (the one after the last completed step); -1 for NULL. */
+BMO_ATTN_API int64_t bmo_attn_session_pos(bmo_attn_session_t *s);
+
+/* The handle's HIP stream (hipStream_t as void*). */
+BMO_ATTN_API void *bmo_attn_session_stream(bmo_attn_session_t *s);
+
+/* One token step at position pos (0 <= pos <= 2^31 - 2; any position, not
+ * only the next one, as bmo_forward_temporal2 takes it,
+ * src/bmo_api.cpp:365-511), launched eagerly on the handle's stream;
+ * returns when out is written.  Afterwards the position is pos + 1. */
+BMO_ATTN_API int bmo_attn_session_forward(bmo_attn_session_t *s, int pos, const float *q,
+                                          const float *k, const float *v, float *out);
+
+/* Records one token step over these buffers into a HIP graph (replacing a
+ * previous one); the graph reads the position from device memory and ends
+ * by advancing it.  Nothing runs and the position does not change.  The
+ * buffers must stay valid while the graph is kept.  Stands in for
+ * bmo_capture_graphs (src/bmo_api.cpp:334-351). */
+BMO_ATTN_API int bmo_attn_session_capture(bmo_attn_session_t *s, const float *q, const float *k,
+                                          const float *v, float *out);
+
+/* 1 when a step is captured, else 0 (bmo_has_cuda_graphs,
+ * src/bmo_api.cpp:353-359). */
+BMO_ATTN_API int bmo_attn_session_has_graph(bmo_attn_session_t *s);
+
+/* Replays the captured step at position pos (same range as forward) on the
+ * handle's stream and returns when it is done; the captured buffers hold the
+ * step's q/k/v on entry and its output on return.  Afterwards the position
+ * is pos + 1.  Replaying at the handle's current position costs one graph
+ * launch; another position first sets the device position. */
+BMO_ATTN_API int bmo_attn_session_replay(bmo_attn_session_t *s, int pos);
+
+/* Message of the handle's most recent failed call, or (s == NULL) of the
+ * calling thread's last failed create; NULL if none.  Owned by the library,
+ * valid until the next call on the handle (src/bmo_api.h:142-145). */
+BMO_ATTN_API const char *bmo_attn_session_last_error(bmo_attn_session_t *s);
 
 /* ---- Q4_0 weight GEMV (the projections around attention) -------------------- */
 
