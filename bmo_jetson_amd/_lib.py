@@ -37,6 +37,7 @@ SIGNATURES = {
     "bmo_positions_advance": (i32, [P, i32, i32, P]),
     "bmo_kv_ring_write": (i32, [P, i32, i32, i64, i32, P, P, P]),
     "bmo_kv_ring_prefill": (i32, [P, i32, i32, P, P, i32, i32, P, P, P, P, f32, P]),
+    "bmo_kv_ring_prefill_noalloc": (i32, [P, i32, i32, P, P, i32, i32, P, P, P, P, f32, P]),
     "bmo_kv_ring_copy_k_f32": (i32, [P, i32, i32, i32, i32, P, i32]),
     "bmo_kv_ring_export_q4_0": (i64, [P, i32, i32, i32, i32, i32, P, i64]),
     "bmo_kv_ring_import_q4_0": (i64, [P, i32, i32, i32, i32, i32, P, i64]),

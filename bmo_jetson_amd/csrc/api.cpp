@@ -419,12 +419,45 @@ int bmo_kv_ring_write(bmo_kv_ring_t *r, int layer, int session, int64_t pos0, in
     }
 }
 
-int bmo_kv_ring_prefill(bmo_kv_ring_t *r, int layer, int n_batch, const int *session_ids,
-                        const int *pos0, int n_tok, int n_heads, const uint16_t *q,
-                        const uint16_t *k, const uint16_t *v, float *out, float scale,
-                        void *stream) {
+}  // extern "C"
+
+namespace {
+
+// Staging of bmo_kv_ring_prefill_noalloc: a fixed array in each device's
+// global memory (the library holds it until the process ends), shared by
+// every such call on that device.  Host code uses the per-device address
+// from hipGetSymbolAddress, never the array's name (which is a host-side
+// stand-in).  Staged blocks are written by the stage kernel of the same call
+// before anything reads them (padding slots are read only under a zero
+// scale and a mask), so nothing needs clearing between calls.
+constexpr int64_t kNoAllocScratchBytes = int64_t(32) << 20;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+std::mutex g_scratch_mu;
+uint8_t *g_scratch_ptr[kMaxDevices] = {};
+
+// The scratch address on `device` (which must be current), looked up once
+// per device; nullptr with *err set on failure.
+uint8_t *scratch_on(int device, hipError_t *err) {
+    *err = hipSuccess;
+    if (device < 0 || device >= kMaxDevices) {
+        *err = hipErrorInvalidDevice;
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[device]) {
+        void *ptr = nullptr;
+        *err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (*err != hipSuccess) return nullptr;
+        g_scratch_ptr[device] = static_cast<uint8_t *>(ptr);
+    }
+    return g_scratch_ptr[device];
+}
+
+int prefill_common(bmo_kv_ring_t *r, const char *fn, bool noalloc, int layer, int n_batch,
+                   const int *session_ids, const int *pos0, int n_tok, int n_heads, const uint16_t *q,
+                   const uint16_t *k, const uint16_t *v, float *out, float scale, void *stream) {
     if (!r) return BMO_ATTN_ERR_NULL;
-    const char *fn = "bmo_kv_ring_prefill";
     try {
         if (!pos0 || !q || !k || !v || !out)
             return fail(r, BMO_ATTN_ERR_NULL, std::string(fn) + ": null pointer argument");
@@ -462,23 +495,38 @@ int bmo_kv_ring_prefill(bmo_kv_ring_t *r, int layer, int n_batch, const int *ses
         p.qscale = scale * kLog2e;
         p.sg = bmo::make_geom(1, n_batch, r->g.n_kv_heads, r->g.head_dim, n_tok);
         const int64_t need = bmo::prefill_is_direct(p) ? 0 : p.sg.total_bytes();
-        // Staged calls on one ring share its staging buffer: they must be
-        // ordered on one stream (the lock only guards the buffer's growth).
-        std::lock_guard<std::mutex> stage_lock(r->stage_mu);
-        if (need > r->stage_bytes) {
-            // grow-only staging; the previous one may still be read by queued work
-            hipError_t e = hipStreamSynchronize((hipStream_t) stream);
-            if (e == hipSuccess && r->stage) e = hipFree(r->stage);
-            r->stage = nullptr;
-            r->stage_bytes = 0;
-            if (e == hipSuccess) e = hipMalloc(&r->stage, (size_t) need);
-            if (e != hipSuccess) {
-                r->stage = nullptr;
-                return hip_fail(r, e, "bmo_kv_ring_prefill: staging allocation");
+        std::unique_lock<std::mutex> stage_lock(r->stage_mu, std::defer_lock);
+        if (noalloc) {
+            if (need > kNoAllocScratchBytes)
+                return fail(r, BMO_ATTN_ERR_ARG,
+                            std::string(fn) + ": the staged chunk needs " + std::to_string(need) +
+                                " bytes (n_batch * n_kv_heads * ceil(n_tok / (2048 / head_dim)) * "
+                                "2304), more than the " + std::to_string(kNoAllocScratchBytes) +
+                                "-byte scratch");
+            if (need > 0) {
+                hipError_t e;
+                p.stage = scratch_on(r->device, &e);
+                if (!p.stage) return hip_fail(r, e, (std::string(fn) + ": scratch address").c_str());
             }
-            r->stage_bytes = need;
+        } else {
+            // Staged calls on one ring share its staging buffer: they must be
+            // ordered on one stream (the lock only guards the buffer's growth).
+            stage_lock.lock();
+            if (need > r->stage_bytes) {
+                // grow-only staging; the previous one may still be read by queued work
+                hipError_t e = hipStreamSynchronize((hipStream_t) stream);
+                if (e == hipSuccess && r->stage) e = hipFree(r->stage);
+                r->stage = nullptr;
+                r->stage_bytes = 0;
+                if (e == hipSuccess) e = hipMalloc(&r->stage, (size_t) need);
+                if (e != hipSuccess) {
+                    r->stage = nullptr;
+                    return hip_fail(r, e, "bmo_kv_ring_prefill: staging allocation");
+                }
+                r->stage_bytes = need;
+            }
+            p.stage = r->stage;
         }
-        p.stage = r->stage;
         if (!bmo::launch_prefill(p, (hipStream_t) stream))
             return fail(r, BMO_ATTN_ERR_ARG, std::string(fn) + ": unsupported head_dim");
         hipError_t e = hipGetLastError();
@@ -488,6 +536,26 @@ int bmo_kv_ring_prefill(bmo_kv_ring_t *r, int layer, int n_batch, const int *ses
     } catch (...) {
         return fail(r, BMO_ATTN_ERR_INTERNAL, std::string(fn) + ": unknown exception");
     }
+}
+
+}  // namespace
+
+extern "C" {
+
+int bmo_kv_ring_prefill(bmo_kv_ring_t *r, int layer, int n_batch, const int *session_ids,
+                        const int *pos0, int n_tok, int n_heads, const uint16_t *q,
+                        const uint16_t *k, const uint16_t *v, float *out, float scale,
+                        void *stream) {
+    return prefill_common(r, "bmo_kv_ring_prefill", false, layer, n_batch, session_ids, pos0, n_tok,
+                          n_heads, q, k, v, out, scale, stream);
+}
+
+int bmo_kv_ring_prefill_noalloc(bmo_kv_ring_t *r, int layer, int n_batch, const int *session_ids,
+                                const int *pos0, int n_tok, int n_heads, const uint16_t *q,
+                                const uint16_t *k, const uint16_t *v, float *out, float scale,
+                                void *stream) {
+    return prefill_common(r, "bmo_kv_ring_prefill_noalloc", true, layer, n_batch, session_ids, pos0,
+                          n_tok, n_heads, q, k, v, out, scale, stream);
 }
 
 int bmo_kv_ring_copy_k_f32(bmo_kv_ring_t *r, int layer, int session, int t_start, int n_positions,

@@ -215,6 +215,23 @@ BMO_ATTN_API int bmo_kv_ring_prefill(bmo_kv_ring_t *ring, int layer, int n_batch
                                      const uint16_t *k, const uint16_t *v,
                                      float *out, float scale, void *stream);
 
+/* bmo_kv_ring_prefill that allocates nothing, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  Same
+ * arguments, results and errors as bmo_kv_ring_prefill; a staged call (GQA, or
+ * more than 256 tokens) stages the chunk in a fixed 32 MiB array that each
+ * GPU holds for the life of the process, instead of the ring's growable
+ * buffer.  A staged chunk needing more than 32 MiB (n_batch * n_kv_heads *
+ * ceil(n_tok / (2048 / head_dim)) * 2304 bytes) is rejected with
+ * BMO_ATTN_ERR_ARG and nothing is launched.  Every call on one GPU shares
+ * that GPU's array: calls that overlap on one GPU (on different streams or
+ * from different threads) race and must be ordered by the caller. */
+BMO_ATTN_API int bmo_kv_ring_prefill_noalloc(bmo_kv_ring_t *ring, int layer, int n_batch,
+                                             const int *session_ids, const int *pos0,
+                                             int n_tok, int n_heads, const uint16_t *q,
+                                             const uint16_t *k, const uint16_t *v,
+                                             float *out, float scale, void *stream);
+
 /* ---- readout / export ------------------------------------------------------- */
 
 /* Copies slots [t_start, t_start+n_positions) of layer's K for one session as
