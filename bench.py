@@ -201,8 +201,13 @@ def bench_b1(torch, iters=200):
                      "eager_us": round(eager_us, 3)}
     ring.close()
     b = unit_bytes(H, D, W)
+    cold = bench_b1_cold(torch)
     return {
         "workload": "cfg1: S=1 L=1 H=32 D=128 W=512 pos=700",
+        "us_per_layer_cold_32L_fused_graph": cold["fused"],
+        "us_per_layer_cold_32L_decode_graph": cold["decode"],
+        "cold_note": cold["note"],
+        "graph_launch_floor_us": graph_launch_floor_us(torch),
         "us_per_layer_fused_graph": res["fused"]["graph_us"],
         "us_per_layer_fused_eager": res["fused"]["eager_us"],
         "us_per_layer_fused_rope_graph": res["fused_rope"]["graph_us"],
@@ -211,6 +216,56 @@ def bench_b1(torch, iters=200):
         "decode_GBps_graph": round(b / (res["decode"]["graph_us"] * 1e-6) / 1e9, 1),
         "target_us": 10.0,
     }
+
+
+def graph_launch_floor_us(torch, calls=200):
+    """Microseconds per launch of a graph of `calls` launches of a kernel with
+    no work to speak of (the library's position advance on one int): the
+    floor under any per-call latency measured from a graph on this box."""
+    from bmo_jetson_amd import positions_advance
+    dummy = torch.zeros(1, dtype=torch.int32, device="cuda")
+    return round(graph_us_per_call(torch, lambda st: positions_advance(dummy, 1, 0, stream=st),
+                                   calls), 3)
+
+
+def bench_b1_cold(torch, replicas=8):
+    """BASELINE config 1 as a model step runs it: 32 layers (one launch each,
+    32 distinct layer windows) at B=1, with the ring held `replicas` times
+    (612 MB) and consecutive steps on consecutive replicas, so that each
+    layer's 2.4 MB window has left the 256 MB last-level cache before it is
+    read again (in the model, the weights streamed between layers evict it).
+    Microseconds per launch from HIP-graph replays of `replicas` steps."""
+    from bmo_jetson_amd import KVRing
+
+    H, D, W, P, L = 32, 128, 512, 700, 32
+    ring = KVRing(L, replicas, H, D, W)
+    fill_ring(torch, ring, L, replicas, H, D, W, np.full(replicas, P), 0xB0A00011, outlier_p=0.0)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0xB0A00011)
+    q = torch.randn((L, H * D), device="cuda", generator=g)
+    k = torch.randn((L, H * D), device="cuda", generator=g)
+    v = torch.randn((L, H * D), device="cuda", generator=g)
+    out = torch.empty((L, H * D), device="cuda")
+    pos = torch.tensor([P], dtype=torch.int32, device="cuda")
+    sids = [torch.tensor([r], dtype=torch.int32, device="cuda") for r in range(replicas)]
+    res = {}
+    for name in ("fused", "decode"):
+        def steps(st, name=name):
+            for r in range(replicas):
+                for layer in range(L):
+                    if name == "fused":
+                        ring.append_decode(layer, pos, q[layer], k[layer], v[layer], out[layer], H,
+                                           session_ids=sids[r], stream=st)
+                    else:
+                        ring.decode(layer, pos, q[layer], out[layer], H, session_ids=sids[r],
+                                    stream=st)
+        steps(torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        res[name] = round(graph_us_per_call(torch, steps, 1, reps=10) / (replicas * L), 3)
+    ring.close()
+    res["note"] = (f"{replicas} ring replicas x {L} layers ({replicas * L * unit_bytes(H, D, W) / 1e6:.0f}"
+                   " MB), one replica per step: every window is read from HBM")
+    return res
 
 
 def bench_depformer(torch, frames=20):
@@ -250,6 +305,7 @@ def bench_depformer(torch, frames=20):
     return {
         "workload": "cfg2: depformer L=6 H=16 D=64 W=8, 8 steps per frame, reset + fused "
                     "append+decode",
+        "graph_launch_floor_us": graph_launch_floor_us(torch),
         "us_per_frame_graph": round(us_frame, 3),
         "us_per_call_graph": round(us_frame / (STEPS * L), 3),
         "calls_per_frame": STEPS * L,
@@ -426,7 +482,10 @@ def cpu_baseline(torch, ring, L, S, H, D, W, pos_host, q_dev, out_dev, budget_s)
     output of those sessions."""
     import oracle
 
-    n_threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    # The GPU box grants one GPU's job a share of 16 host CPUs, whatever the
+    # affinity mask or nproc show; the pool is sized to that share.
+    host_cpus = len(os.sched_getaffinity(0))
+    n_threads = max(1, min(16, host_cpus))
 
     def stripes(n):
         kc = np.zeros((n, H, W, D // 32), dtype=oracle.BLOCK_DTYPE)
@@ -455,6 +514,9 @@ def cpu_baseline(torch, ring, L, S, H, D, W, pos_host, q_dev, out_dev, budget_s)
         "value": round(bytes_mt / secs / 1e9, 3),
         "unit": "GB/s",
         "cores": n_threads,
+        "host_cpus_visible": host_cpus,
+        "nproc": os.cpu_count(),
+        "cores_note": "threads used = the 16-CPU share the GPU box grants one GPU's job",
         "kind": "port",
         "sample": f"layer 0 of the cfg3 ring, {n_sess} sessions x {H} heads x W={W}, "
                   f"{iters} pass(es), {n_threads} threads, {secs:.1f} s",

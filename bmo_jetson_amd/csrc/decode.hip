@@ -607,13 +607,15 @@ struct Shape {
 // Workgroup shape per call: one wave per (entry, head) unit with two groups
 // of loads in flight when there are enough units to fill the chip (measured
 // best over sustained runs of BASELINE config 3), else enough waves per unit
-// for about 512 waves in all.  Below 128 units a plain decode uses 4 waves
-// per unit and a fused one 8 (B=1, 32 units: 5.48 vs 5.68 us plain, 6.05 vs
-// 6.12 us fused, where wave 0 takes the new token).  BMO_ATTN_SHAPE = "nw,pf"
-// overrides the choice (tuning; unknown shapes fall back to the default).
+// for about 512 waves in all.  Below 128 units, 8 waves per unit (B=1, 32
+// units, over a 32-layer model step whose windows come from HBM: 6.86 us
+// plain and 7.03 us fused per layer, against 7.44 and 8.16 us with 4 waves;
+// fused, wave 0 takes the new token).  BMO_ATTN_SHAPE = "nw,pf" overrides
+// the choice (tuning; unknown shapes fall back to the default).
 Shape pick_shape(int64_t units, int n_groups, bool fused) {
+    (void) fused;
     Shape s{1, 2};
-    if (units < 128) s = fused ? Shape{8, 1} : Shape{4, 1};
+    if (units < 128) s = Shape{8, 1};
     else if (units < 256) s = Shape{4, 1};
     else if (units < 512) s = Shape{2, 1};
     while (s.nw > 1 && s.nw > n_groups) s.nw /= 2;  // no more waves than groups

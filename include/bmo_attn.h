@@ -203,7 +203,11 @@ BMO_ATTN_API int bmo_kv_ring_append_decode_rope(bmo_kv_ring_t *ring, int layer, 
  *   out:  [n_batch][n_tok][n_heads][head_dim] fp32
  * Attention runs on matrix cores: K, V and the softmax weights in fp16 (K and
  * V values must lie in fp16 range, as the reference's F16 cache requires),
- * q from its bf16 values, fp32 accumulation.  With n_heads == n_kv_heads and
+ * q from its bf16 values times scale * log2(e) rounded to fp16, fp32
+ * accumulation.  So |q| * scale * log2(e) must stay below 65504 (|q| below
+ * about 5.1e5 at head_dim 128 with the default scale); a query with a larger
+ * element gets a non-finite output row, and the other queries are
+ * unaffected.  With n_heads == n_kv_heads and
  * n_tok <= 256 one kernel quantizes, attends and commits; otherwise the call
  * stages the chunk's Q4_0 blocks in the ring's staging buffer (n_batch *
  * n_kv_heads stripes of n_tok slots), grown on first use with a
