@@ -65,6 +65,7 @@ def lib() -> ctypes.CDLL:
             "orc_round_bf16": (ctypes.c_float, [ctypes.c_float]),
             "orc_cpu_decode_f32": (None, [P, P, i32, i32, i32, i32, i64, P, P, P]),
             "orc_cpu_baseline_run": (f64, [P, P, i32, i32, i32, i32, i32, P, P, P, i32, i32]),
+            "orc_cpu_ggml_style_run": (f64, [P, P, i32, i32, i32, i32, i32, P, P, P, i32, i32]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -266,4 +267,18 @@ def cpu_baseline_run(kc, vc, pos: np.ndarray, q: np.ndarray, n_heads: int,
     out = np.zeros((n_sess, n_heads, d), dtype=np.float32)
     secs = lib().orc_cpu_baseline_run(_p(kc), _p(vc), n_sess, n_heads, n_kv, d, n_ctx,
                                       _p(pos), _p(q), _p(out), n_threads, iters)
+    return float(secs), out
+
+
+def cpu_ggml_style_run(kc, vc, pos: np.ndarray, q: np.ndarray, n_heads: int,
+                       n_threads: int, iters: int):
+    """The ggml-style SIMD baseline (Q8_0 q, Q4_0 x Q8_0 dots, online softmax):
+    same arguments and result as cpu_baseline_run."""
+    n_sess, n_kv, n_ctx, nblk = kc.shape
+    d = nblk * 32
+    pos = np.ascontiguousarray(pos, dtype=np.int64)
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    out = np.zeros((n_sess, n_heads, d), dtype=np.float32)
+    secs = lib().orc_cpu_ggml_style_run(_p(kc), _p(vc), n_sess, n_heads, n_kv, d, n_ctx,
+                                        _p(pos), _p(q), _p(out), n_threads, iters)
     return float(secs), out

@@ -183,6 +183,15 @@ double orc_cpu_baseline_run(const orc_block_q4_0 *kc, const orc_block_q4_0 *vc,
                             const float *q, float *out, int n_threads,
                             int iters);
 
+/* A SIMD baseline restating ggml's CPU flash attention over Q4_0 K/V
+ * (cpu_ggml_style.c): q to Q8_0, Q4_0 x Q8_0 dot products, online softmax
+ * with expf, V dequantized to fp32.  Same arguments and result as
+ * orc_cpu_baseline_run. */
+double orc_cpu_ggml_style_run(const orc_block_q4_0 *kc, const orc_block_q4_0 *vc, int n_sess,
+                              int n_heads, int n_kv_heads, int head_dim, int n_ctx,
+                              const int64_t *pos, const float *q, float *out, int n_threads,
+                              int iters);
+
 #ifdef __cplusplus
 }
 #endif
