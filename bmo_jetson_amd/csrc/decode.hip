@@ -61,9 +61,9 @@
 // rotations, rows go through LDS and the workgroup's threads merge waves.
 //
 // Fused append (the reference's write-then-attend,
-// src/bmo_cuda_kernels.cu:749-754): the current token's K/V rows are quantized
-// in registers with the bit-exact quantizer (the K blocks by lanes 0..LPK-1,
-// the V blocks by the next LPK lanes), wave 0 attends to that key from
+// src/bmo_cuda_kernels.cu:749-754): wave 0 quantizes the current token's K/V
+// rows in registers with the bit-exact quantizer, spread over all 64 lanes
+// (32 / LPK lanes per block, reductions by DPP), attends to that key from
 // registers, and the first query head of each kv group stores the blocks to
 // slot pos % n_ctx.  Every workgroup masks that slot out of its ring reads.
 #include <math.h>
@@ -317,15 +317,15 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     const int blk = lane % LPK;
 
     const int unit = blockIdx.x;
-    const int b = unit / p.n_heads;
+    const int b = (int) p.div_heads.div((uint32_t) unit);
     const int h = unit - b * p.n_heads;
 
     const RingGeom &g = p.g;
     const int sid_in = p.session_ids ? p.session_ids[b] : b;
     const bool sid_ok = sid_in >= 0 && sid_in < g.n_sessions;
     const int sid = sid_ok ? sid_in : 0;  // an in-bounds stripe for loads issued before the check
-    const int q_per_kv = p.n_heads / p.n_kv;
-    const int kvh = h / q_per_kv;
+    const int q_per_kv = p.q_per_kv;
+    const int kvh = (int) p.div_qkv.div((uint32_t) h);
     uint8_t *stripe = p.base + g.stripe_offset(p.layer, sid, kvh);
     float *out_row = p.out + (int64_t) unit * D;
 
@@ -367,13 +367,34 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
         for (int j = 0; j < NB - 1; ++j) load_clamped(j, buf[j]);
         prep_load<D>(p.q + (int64_t) unit * D, lane, q_lo, q_hi);
     }
+    // Fused: wave 0 holds the current token's K and V rows spread over its
+    // lanes for the lane-parallel quantizer, BL lanes per block: lane l
+    // takes block nb = l / BL (K block nb for nb < LPK, else V block
+    // nb - LPK), elements gi*NE/2 + t and gi*NE/2 + t + 16 of it (t < NE/2),
+    // gi = l % BL.  Requested before the position, which they do not need.
+    constexpr int BL = 32 / LPK;
+    constexpr int NE = LPK;
+    const int nb = lane / BL;
+    const int gi = lane % BL;
+    float xnew[NE];
+    if constexpr (FUSED) {
+        if (wave == 0) {
+            const float *src = (nb < LPK ? p.k_new : p.v_new) + ((int64_t) b * p.n_kv + kvh) * D +
+                               (nb % LPK) * kQK + gi * (NE / 2);
+#pragma unroll
+            for (int t = 0; t < NE / 2; ++t) {
+                xnew[t] = src[t];
+                xnew[NE / 2 + t] = src[16 + t];
+            }
+        }
+    }
     const int pos = p.pos ? p.pos[b] : p.pos_scalar;
     if (!sid_ok || pos < 0) {
         for (int i = threadIdx.x; i < D; i += blockDim.x) out_row[i] = 0.0f;
         return;
     }
     const int window = (int) min((int64_t) pos + 1, (int64_t) g.n_ctx);
-    const int cur = pos % g.n_ctx;
+    const int cur = pos - (int) p.div_ctx.div((uint32_t) pos) * g.n_ctx;  // pos % n_ctx
     const int n_grp = (window + G - 1) / G;
     g0 = ww < 0 ? 0 : ww * n_grp / NWW;
     n_it = ww < 0 ? 0 : (ww + 1) * n_grp / NWW - g0;
@@ -381,15 +402,6 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
 #pragma unroll
         for (int j = 0; j < NB - 1; ++j) load_clamped(j, buf[j]);
         prep_load<D>(p.q + (int64_t) unit * D, lane, q_lo, q_hi);
-    }
-    // Fused: wave 0's lane blk (kk == 0) holds K block blk of the current
-    // token, lane LPK + blk (kk == 1) its V block; loaded here so that their
-    // latency overlaps the query's.
-    float xnew[kQK];
-    if constexpr (FUSED) {
-        if (wave == 0 && kk < 2)
-            load_block_f32((kk == 0 ? p.k_new : p.v_new) + ((int64_t) b * p.n_kv + kvh) * D + blk * kQK,
-                           xnew);
     }
     if (p.rope) rope_table<D>(pos, p.rope_r, lane, s_rope[wave]);  // wave-private LDS
     prep_digits<D>(q_lo, q_hi, p.qscale, lane, s_dig[wave], s_sq[wave], p.rope ? s_rope[wave] : nullptr);
@@ -420,32 +432,70 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
 
     if constexpr (FUSED) {
         if (wave == 0) {
-            // The current token's blocks: lane blk (kk == 0) quantizes K block
-            // blk, lane LPK + blk (kk == 1) V block blk; the V codes and scale
-            // then move to lane blk, which attends to the new key.
-            uint32_t qs[4] = {0u, 0u, 0u, 0u};
-            uint32_t d16 = 0;
-            if (kk < 2) {
-                if (p.rope && kk == 0) {
+            // The current token's blocks, quantized by the whole wave (BL
+            // lanes per block); the K and V codes and scales of block blk
+            // then move to lane blk (kk == 0), which attends to the new key.
+            constexpr int HE = NE / 2;
+            constexpr int LPD = 4 / HE;  // lanes per code dword
+            if (p.rope) {
+                // K pairs (2m, 2m+1) of the head turn by table entry m
+                const float2 *tab = s_rope[0] + (nb % LPK) * 16;
+                if constexpr (HE == 2) {
+                    float a0 = xnew[0], b0 = xnew[1], a1 = xnew[2], b1 = xnew[3];
+                    rope_pair(a0, b0, tab[gi]);
+                    rope_pair(a1, b1, tab[gi + 8]);
+                    if (nb < LPK) {
+                        xnew[0] = a0;
+                        xnew[1] = b0;
+                        xnew[2] = a1;
+                        xnew[3] = b1;
+                    }
+                } else {
+                    // elements gi and gi + 16: each pair spans lanes gi, gi ^ 1
+                    const bool odd = gi & 1;
 #pragma unroll
-                    for (int m = 0; m < kQK / 2; ++m)
-                        rope_pair(xnew[2 * m], xnew[2 * m + 1], s_rope[0][blk * 16 + m]);
+                    for (int t = 0; t < 2; ++t) {
+                        const float x = xnew[t];
+                        const float y = dpp<0xB1>(x);  // the other element of the pair
+                        const float2 cs = tab[gi / 2 + 8 * t];
+                        // (a, b) -> (a c - b s, a s + b c), products rounded apart
+                        const float r = odd ? y * cs.y + x * cs.x : x * cs.x - y * cs.y;
+                        if (nb < LPK) xnew[t] = r;
+                    }
                 }
-                uint16_t d;
-                quantize_block_q4_0(xnew, d, qs);
-                d16 = d;
-                if (h % q_per_kv == 0) store_block(stripe, g, cur, blk, kk, d, qs);
             }
-            // lane blk receives lane LPK + blk's V block
-            uint32_t vq[4];
+            uint16_t d16;
+            const uint32_t dw = quantize_block_q4_0_lanes<BL>(xnew, gi, d16);
+            if (h == kvh * q_per_kv) {  // the first query head of the kv group
+                // the first lane of each code dword stores it, lane 0 of the
+                // block the scale (ring_layout.hpp: K codes as code ^ 8)
+                // (the offsets of RingGeom::kcode_offset / vcode_offset /
+                // scale_offset, with this kernel's compile-time G)
+                const int which = nb < LPK ? 0 : 1;
+                const int bb = nb % LPK;
+                uint8_t *grp = stripe + (int64_t) ((unsigned) cur / G) * g.group_stride;
+                const int key = (int) ((unsigned) cur % G);
+                if (gi % LPD == 0)
+                    *reinterpret_cast<uint32_t *>(grp + which * kVCodeOff + key * (D / 2) + bb * 16 +
+                                                  4 * (gi / LPD)) = which == 0 ? dw ^ 0x88888888u : dw;
+                if (gi == 0)
+                    reinterpret_cast<uint16_t *>(grp + kScaleOff + (key * LPK + bb) * 4)[which] = d16;
+            }
+            // lane blk gathers K block blk (lanes blk*BL + c*LPD) and V block
+            // blk (lanes (LPK + blk)*BL + c*LPD)
+            uint32_t kq[4], vq[4];
 #pragma unroll
-            for (int c = 0; c < 4; ++c) vq[c] = (uint32_t) __shfl((int) qs[c], lane + LPK);
-            const uint32_t vd16 = (uint32_t) __shfl((int) d16, lane + LPK);
+            for (int c = 0; c < 4; ++c) {
+                kq[c] = (uint32_t) __shfl((int) dw, blk * BL + c * LPD);
+                vq[c] = (uint32_t) __shfl((int) dw, (LPK + blk) * BL + c * LPD);
+            }
+            const uint32_t kd16 = (uint32_t) __shfl((int) d16, blk * BL);
+            const uint32_t vd16 = (uint32_t) __shfl((int) d16, (LPK + blk) * BL);
             float s_new = 0.0f;
             if (kk == 0) {
-                const uint4 kflip = make_uint4(qs[0] ^ 0x88888888u, qs[1] ^ 0x88888888u,
-                                               qs[2] ^ 0x88888888u, qs[3] ^ 0x88888888u);
-                s_new = f16_bits_to_f32(d16) * score(kflip);
+                const uint4 kflip = make_uint4(kq[0] ^ 0x88888888u, kq[1] ^ 0x88888888u,
+                                               kq[2] ^ 0x88888888u, kq[3] ^ 0x88888888u);
+                s_new = f16_bits_to_f32(kd16) * score(kflip);
             }
             s_new = key_sum<LPK>(s_new);
             if (kk == 0) {
@@ -647,9 +697,14 @@ bool launch_shape(const DecodeParams &p, bool fused, hipStream_t stream, const S
 
 }  // namespace
 
-bool launch_decode(const DecodeParams &p, bool fused, hipStream_t stream) {
-    const int64_t units = (int64_t) p.n_batch * p.n_heads;
+bool launch_decode(const DecodeParams &params, bool fused, hipStream_t stream) {
+    const int64_t units = (int64_t) params.n_batch * params.n_heads;
     if (units <= 0) return true;
+    DecodeParams p = params;
+    p.q_per_kv = p.n_heads / p.n_kv;
+    p.div_heads = make_fastdiv((uint32_t) p.n_heads);
+    p.div_qkv = make_fastdiv((uint32_t) p.q_per_kv);
+    p.div_ctx = make_fastdiv((uint32_t) p.g.n_ctx);
     const Shape s = pick_shape(units, p.g.n_groups, fused);
     if (p.g.head_dim == 128) {
         if (!launch_shape<128>(p, fused, stream, s)) launch_variant<128, 1, 1>(p, fused, stream);

@@ -27,6 +27,26 @@ struct AppendParams {
     const float *v;
 };
 
+// Division by a run-time constant d in [1, 2^31) of numerators n in
+// [0, 2^31) without the integer-division sequence (Granlund and Montgomery,
+// "Division by invariant integers using multiplication", 1994, section 4:
+// with s = ceil(log2 d) and m = floor(2^32 (2^s - d) / d) + 1, n / d equals
+// (mulhi(n, m) + n) >> s; mulhi(n, m) < n keeps the sum below 2^32).
+struct FastDiv {
+    uint32_t m;
+    uint32_t s;
+    __host__ __device__ uint32_t div(uint32_t n) const {
+        return ((uint32_t) (((uint64_t) n * m) >> 32) + n) >> s;
+    }
+};
+
+inline FastDiv make_fastdiv(uint32_t d) {
+    uint32_t s = 0;
+    while ((uint64_t(1) << s) < d) ++s;
+    const uint64_t m = ((uint64_t(1) << 32) * ((uint64_t(1) << s) - d)) / d + 1;
+    return FastDiv{(uint32_t) m, s};
+}
+
 struct DecodeParams {
     uint8_t *base;  // ring allocation; the fused path writes the current slot
     RingGeom g;
@@ -45,6 +65,10 @@ struct DecodeParams {
     float qscale;        // softmax scale * log2(e)
     int rope;            // nonzero: rotate q (and the fused k_new) by interleaved RoPE at pos
     double rope_r;       // theta^(-2/head_dim): pair i turns by pos * rope_r^i
+    // set by launch_decode: n_heads / n_kv and dividers by n_heads, by
+    // n_heads / n_kv and by g.n_ctx
+    int q_per_kv;
+    FastDiv div_heads, div_qkv, div_ctx;
 };
 
 // Chunked prefill of n_tok tokens per batch entry (prefill.hip).

@@ -133,6 +133,90 @@ __device__ __forceinline__ void quantize_block_q4_0(const float (&x)[kQK], uint1
     }
 }
 
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t) __builtin_amdgcn_mov_dpp((int) v, CTRL, 0xF, 0xF, true);
+}
+
+// Reductions over an aligned group of BL = 8 or 16 lanes of one 16-lane row:
+// lane ^ 1 and lane ^ 2 (quad_perm), then the mirrored quad of the half-row
+// (row_half_mirror) and, for 16, the mirrored half-row (row_mirror).  Every
+// lane of the group must be active.
+template <int BL>
+__device__ __forceinline__ uint32_t group_max_u32(uint32_t v) {
+    v = max(v, dpp_u32<0xB1>(v));
+    v = max(v, dpp_u32<0x4E>(v));
+    v = max(v, dpp_u32<0x141>(v));
+    if constexpr (BL == 16) v = max(v, dpp_u32<0x140>(v));
+    return v;
+}
+template <int BL>
+__device__ __forceinline__ uint32_t group_min_u32(uint32_t v) {
+    v = min(v, dpp_u32<0xB1>(v));
+    v = min(v, dpp_u32<0x4E>(v));
+    v = min(v, dpp_u32<0x141>(v));
+    if constexpr (BL == 16) v = min(v, dpp_u32<0x140>(v));
+    return v;
+}
+
+// Lane-parallel quantization of one block spread over BL = 8 or 16
+// consecutive lanes (the group starts at a multiple of BL): lane i of the
+// group holds E = 32 / BL elements, x[t] = element i*E/2 + t and
+// x[E/2 + t] = element i*E/2 + t + 16 (t < E/2), so its codes fill E/2 whole
+// bytes of the block.  Bit-identical to quantize_block_q4_0_literal for every
+// input:
+//   M = the largest |x_j| over non-NaN elements, 0 if there is none (from the
+//   fp32 bit patterns, which order non-negative values as unsigned integers);
+//   vmax = the first x_j with |x_j| == M, +0 when M == 0: the literal form's
+//   scan "if (amax < |x_j|)" from amax = +0 keeps exactly that element (a NaN
+//   never compares greater, a tie never replaces an earlier element), and
+//   its sign comes from a group minimum over keys 2 j + sign;
+//   d, id and each code as the literal form computes them.
+// Returns code dword i*E/8 of the block (bytes 4c..4c+3), assembled in every
+// lane that contributes to it, and the fp16 scale bits in d16.
+template <int BL>
+__device__ __forceinline__ uint32_t quantize_block_q4_0_lanes(const float (&x)[32 / BL], int i,
+                                                              uint16_t &d16) {
+#pragma clang fp contract(off)
+    constexpr int E = 32 / BL, HE = E / 2;
+    uint32_t a[E];
+    uint32_t m = 0;
+#pragma unroll
+    for (int t = 0; t < E; ++t) {
+        const uint32_t ab = __builtin_bit_cast(uint32_t, x[t]) & 0x7FFFFFFFu;
+        a[t] = ab > 0x7F800000u ? 0u : ab;  // a NaN counts as 0
+        m = max(m, a[t]);
+    }
+    const uint32_t M = group_max_u32<BL>(m);
+    uint32_t key = 0xFFFFFFFFu;
+#pragma unroll
+    for (int t = 0; t < E; ++t) {
+        const uint32_t j = (uint32_t) (i * HE + (t < HE ? t : t - HE + 16));
+        const uint32_t k = (j << 1) | (__builtin_bit_cast(uint32_t, x[t]) >> 31);
+        key = a[t] == M ? min(key, k) : key;
+    }
+    const uint32_t K = group_min_u32<BL>(key);
+    const float vmax = M == 0u ? 0.0f : __builtin_bit_cast(float, M | (K << 31));
+    float d = vmax / -8.0f;
+    asm volatile("" : "+v"(d));  // materialize d in fp32 (see the header note)
+    const float id = (d != 0.0f) ? 1.0f / d : 0.0f;
+    d16 = f32_to_f16_bits(d);
+    uint32_t w = 0;
+#pragma unroll
+    for (int t = 0; t < HE; ++t) {
+        int c0 = x86_trunc_to_i8(x[t] * id + 8.5f);
+        int c1 = x86_trunc_to_i8(x[t + HE] * id + 8.5f);
+        c0 = c0 > 15 ? 15 : c0;
+        c1 = c1 > 15 ? 15 : c1;
+        const uint32_t byte = ((uint32_t) c0 | ((uint32_t) c1 << 4)) & 0xFFu;
+        w |= byte << (8 * ((i * HE + t) & 3));
+    }
+    // the 4 / HE lanes of one dword are adjacent
+    w |= dpp_u32<0xB1>(w);
+    if constexpr (HE == 1) w |= dpp_u32<0x4E>(w);
+    return w;
+}
+
 // Loads one block's 32 fp32 elements (16-byte aligned source).
 __device__ __forceinline__ void load_block_f32(const float *__restrict__ src, float (&x)[kQK]) {
     const float4 *s4 = reinterpret_cast<const float4 *>(src);

@@ -164,6 +164,33 @@ def test_fused_append_decode_parity(gpu, n_heads, n_kv, d, n_ctx, pos):
     m.assert_ring_equal(layer, 0)
 
 
+@pytest.mark.parametrize("d,n_ctx,theta", [(128, 48, None), (64, 8, None), (128, 48, 10000.0),
+                                           (64, 8, 500000.0)])
+def test_fused_append_adversarial_bit_exact(gpu, d, n_ctx, theta):
+    """The fused call quantizes the current token's rows with the wave spread
+    over the blocks (BL lanes per block); its ring writes must match the
+    oracle quantizer bit for bit on the adversarial blocks (ties of +max and
+    -max, NaN, infinities, zero and -0 blocks, subnormal and fp16-overflowing
+    scales), with and without RoPE, GQA, one entry per session."""
+    n_sess, n_kv, n_heads = 6, 4, 8
+    m = Mirror(gpu, 1, n_sess, n_kv, d, n_ctx)
+    sids = [4, 0, 5, 2, 1, 3]
+    for step in range(3):
+        pos = [(7 * b + 3 * step) % 50 + step for b in range(n_sess)]
+        k = _adversarial_rows(n_sess * n_kv, d, 300 + step).reshape(n_sess, n_kv, d)
+        v = _adversarial_rows(n_sess * n_kv, d, 400 + step).reshape(n_sess, n_kv, d)
+        q = oracle.normal(500 + step, n_sess * n_heads * d)
+        out = gpu.empty((n_sess * n_heads * d,), dtype=gpu.float32, device="cuda")
+        m.ring.append_decode(0, _i32(gpu, pos), m.dev(q), m.dev(k), m.dev(v), out, n_heads,
+                             session_ids=_i32(gpu, sids), stream=m.stream, rope_theta=theta)
+        for b in range(n_sess):
+            kb = k[b] if theta is None else oracle.rope_interleaved(k[b], pos[b], theta)
+            m.oracle_append(0, sids[b], pos[b], kb, v[b])
+        gpu.cuda.synchronize()
+        for s in range(n_sess):
+            m.assert_ring_equal(0, s)
+
+
 def test_batched_sessions_ids_and_invalid_entries(gpu):
     n_sess, n_heads, d, n_ctx = 7, 8, 128, 96
     m = Mirror(gpu, 1, n_sess, n_heads, d, n_ctx)
