@@ -10,6 +10,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <climits>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -331,6 +332,8 @@ static int decode_common(bmo_kv_ring_t *r, const char *fn, bool fused, int layer
         if (n_heads <= 0 || n_heads % r->g.n_kv_heads != 0)
             return fail(r, BMO_ATTN_ERR_ARG,
                         std::string(fn) + ": n_heads must be a positive multiple of n_kv_heads");
+        if ((int64_t) n_batch * n_heads > INT_MAX)
+            return fail(r, BMO_ATTN_ERR_ARG, std::string(fn) + ": n_batch * n_heads exceeds INT_MAX");
         if (!(scale > 0.0f)) scale = 1.0f / std::sqrt((float) r->g.head_dim);
         if (!std::isfinite(scale))
             return fail(r, BMO_ATTN_ERR_ARG, std::string(fn) + ": scale must be finite");
