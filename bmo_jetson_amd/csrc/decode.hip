@@ -359,14 +359,15 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     auto load_clamped = [&](int it, Grp &T) { load(min(it, g.n_groups - 1 - g0), T); };
     Grp buf[NB];
     float4 q_lo, q_hi;
-    // With one wave per unit the run starts at group 0 whatever the
-    // position, so the first groups and the query are requested before the
-    // position is read (the scalar read's latency then overlaps theirs).
+    // The query does not depend on the position, so it is requested before
+    // the position is read (the scalar read's latency then overlaps its
+    // own); with one wave per unit the run starts at group 0 whatever the
+    // position, so the first groups go out ahead of it as well.
     if constexpr (NW == 1) {
 #pragma unroll
         for (int j = 0; j < NB - 1; ++j) load_clamped(j, buf[j]);
-        prep_load<D>(p.q + (int64_t) unit * D, lane, q_lo, q_hi);
     }
+    prep_load<D>(p.q + (int64_t) unit * D, lane, q_lo, q_hi);
     // Fused: wave 0 holds the current token's K and V rows spread over its
     // lanes for the lane-parallel quantizer, BL lanes per block: lane l
     // takes block nb = l / BL (K block nb for nb < LPK, else V block
@@ -401,7 +402,6 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     if constexpr (NW > 1) {
 #pragma unroll
         for (int j = 0; j < NB - 1; ++j) load_clamped(j, buf[j]);
-        prep_load<D>(p.q + (int64_t) unit * D, lane, q_lo, q_hi);
     }
     if (p.rope) rope_table<D>(pos, p.rope_r, lane, s_rope[wave]);  // wave-private LDS
     prep_digits<D>(q_lo, q_hi, p.qscale, lane, s_dig[wave], s_sq[wave], p.rope ? s_rope[wave] : nullptr);
