@@ -63,7 +63,7 @@ __device__ __forceinline__ uint32_t f32_to_f16(float x) {
 
 }  // namespace
 
-template <int R, int PFD>
+template <int R, int PFD, bool PAD>
 __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
     constexpr int NT = 512;
     constexpr int NB = PFD + 1;  // weight buffers: PFD iterations in flight
@@ -230,13 +230,32 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
         }
     };
     // Buffer of position k: k % NB.  Each step refills the buffer freed by
-    // the step before with position k + PFD (unconditional loads), then
-    // multiplies position k.
-    for (int k = 0; k < n_pos; k += NB) {
+    // the step before with position k + PFD, then multiplies position k.
+    // Steady state: unconditional loads, so each multiply waits for its own
+    // position's loads only.  The last 2 NB - 2 positions: with PAD, loads
+    // stay unconditional (past the wave's last position they re-read it);
+    // without, they go out only while positions remain, so the wave issues
+    // no loads past its last position (they would hold it until they
+    // return), at the price of a conservative wait: a multiply that follows
+    // a conditional load waits for that load as well.  Measured: rows of one
+    // 64-pair iteration (cols <= 4096) without, longer rows with.
+    int k = 0;
+    for (; k + 2 * NB - 2 < n_pos; k += NB) {
 #pragma unroll
         for (int u = 0; u < NB; ++u) {
             load_next(wb[(u + PFD) % NB]);
-            if (k + u < n_pos) multiply(wb[u]);
+            multiply(wb[u]);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < 2 * NB - 2; ++u) {
+        const int kk = k + u;
+        if constexpr (PAD) {
+            load_next(wb[(u + PFD) % NB]);
+            if (kk < n_pos) multiply(wb[u % NB]);
+        } else if (kk < n_pos) {
+            if (kk + PFD < n_pos) load_next(wb[(u + PFD) % NB]);
+            multiply(wb[u % NB]);
         }
     }
 }
@@ -258,8 +277,12 @@ void launch_rows(const GemvParams &p, hipStream_t stream) {
     // One position in flight beside the one being multiplied: 2, 3 and 4
     // were measured slower at every shape (QKV 8.06 / 9.57 / 9.85 us against
     // 7.62; out-proj 5.29 / 6.43 / 7.23 against 4.50).
-    hipLaunchKernelGGL((gemv_kernel<R, 1>), dim3((unsigned) wgs), dim3(512), gemv_lds_bytes(p.cols), stream,
-                       p);
+    if (p.cols > 4096)
+        hipLaunchKernelGGL((gemv_kernel<R, 1, true>), dim3((unsigned) wgs), dim3(512), gemv_lds_bytes(p.cols),
+                           stream, p);
+    else
+        hipLaunchKernelGGL((gemv_kernel<R, 1, false>), dim3((unsigned) wgs), dim3(512), gemv_lds_bytes(p.cols),
+                           stream, p);
 }
 
 }  // namespace
