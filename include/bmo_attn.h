@@ -132,8 +132,8 @@ BMO_ATTN_API const char *bmo_kv_ring_last_error(const bmo_kv_ring_t *ring);
  *                  (src/bmo_cuda_kernels.cu:867)
  * The window of position p is the min(p+1, n_ctx) most recent positions
  * (src/bmo_cuda_kernels.cu:739-743).  n_heads must be a multiple of
- * n_kv_heads; query head h reads kv head h / (n_heads / n_kv_heads)
- * (src/bmo_cuda_kernels.cu:736-737).
+ * n_kv_heads, and n_batch * n_heads at most INT_MAX; query head h reads kv
+ * head h / (n_heads / n_kv_heads) (src/bmo_cuda_kernels.cu:736-737).
  */
 
 /* Quantizes k_new/v_new into slot pos[b] % n_ctx (the KV write of
