@@ -560,6 +560,8 @@ def main():
                     help="skip the BASELINE config 4 leg (fused append + decode, 256 sessions)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only run the cfg5 chunked-prefill leg and print its JSON (profiling)")
+    ap.add_argument("--latency-only", action="store_true",
+                    help="only run the B=1 and depformer legs (rocprof of the latency kernels)")
     ap.add_argument("--gemv-only", action="store_true",
                     help="only run the Q4_0 GEMV leg and print its JSON (profiling)")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
@@ -593,6 +595,9 @@ def main():
         return
     if args.gemv_only:
         print(json.dumps({"gemv": bench_gemv(torch)}), flush=True)
+        return
+    if args.latency_only:
+        print(json.dumps({"b1": bench_b1(torch), "depformer": bench_depformer(torch)}), flush=True)
         return
 
     run = run_decode(torch, args.config, args.steps, args.warmup, args.sessions)
