@@ -57,8 +57,9 @@
 // keys; the result does not depend on the threshold.  Weights are carried
 // times 2^24 (the stored max is m - 24), which is the scale the subnormal
 // V codes need, so one multiply by the V scale makes a key's weight.  At the end every lane
-// is brought to the wave max, lanes sharing a block are summed by DPP
-// rotations, rows go through LDS and the workgroup's threads merge waves.
+// is brought to the wave max, the four 16-lane rows are summed by permlane
+// swaps and the lanes sharing a block by DPP rotations; a one-wave unit
+// stores its output from registers, several waves merge through LDS.
 //
 // Fused append (the reference's write-then-attend,
 // src/bmo_cuda_kernels.cu:749-754): wave 0 quantizes the current token's K/V
@@ -128,6 +129,21 @@ __device__ __forceinline__ float row_sum(float v) {
     v += dpp<0x4E>(v);
     v += dpp<0x124>(v);
     return v + dpp<0x128>(v);
+}
+// v_permlane32_swap / v_permlane16_swap (gfx950) as inline asm: the
+// compiler's builtins for them hand back one register for both halves of the
+// returned pair.  The instruction exchanges lanes 32-63 of a with lanes 0-31
+// of b (permlane32: a = {a rows 0-1, b rows 0-1}, b = {a rows 2-3, b rows
+// 2-3}) or the odd rows of a with the even rows of b (permlane16: a = {a r0,
+// b r0, a r2, b r2}, b = {a r1, b r1, a r3, b r3}).  The s_nop gives the two
+// wait states a swap needs after a VALU write of its operands.
+__device__ __forceinline__ float swap_sum32(float a, float b) {
+    asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    return a + b;
+}
+__device__ __forceinline__ float swap_sum16(float a, float b) {
+    asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    return a + b;
 }
 __device__ __forceinline__ float lane_value(float v, int lane) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
@@ -301,10 +317,9 @@ template <int D, int NW, int PF, bool FUSED>
 __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     constexpr int LPK = D / kQK;   // lanes (blocks) per key
     constexpr int G = 64 / LPK;    // keys per group = per wave iteration
-    constexpr int ROWS = 4;        // 16-lane rows per wave
     constexpr int NB = PF + 1;     // resident groups per wave
 
-    __shared__ __align__(16) float s_acc[NW * ROWS * D];
+    __shared__ __align__(16) float s_acc[NW * D];
     __shared__ __align__(16) uint32_t s_dig[NW][kPlanes * 4 * LPK];
     __shared__ float s_m[NW];
     __shared__ float s_l[NW];
@@ -557,83 +572,79 @@ __global__ __launch_bounds__(64 * NW) void decode_kernel(DecodeParams p) {
     }
 
     // Bring every lane to the wave max (the factor is folded into one fma
-    // per element), undo the 2^-20 scale of elements 16..31, fold the -8
-    // code offset, and sum the lanes of each row that share a block.
+    // per element), undo the 2^-20 scale of elements 16..31 and fold the -8
+    // code offset.
     const float m_wave = wave_max(mm);
     const float f = __builtin_amdgcn_exp2f(mm - m_wave);
     const float l_wave = wave_sum(l * f) * (1.0f / LPK);
     const float c8 = (-8.0f / 16777216.0f) * (csum * f);  // -8 * sum of p * d, in acc units
     const float f_hi = f * 0.0625f;
 #pragma unroll
-    for (int e = 0; e < 32; ++e) acc[e] = row_block_sum<LPK>(__builtin_fmaf(acc[e], e < 16 ? f : f_hi, c8));
-    // l_wave is 2^24 times the weight sum: the output divides by it times 2^-24
-    const int row = lane >> 4;
-    if ((lane & 15) < LPK) {
-        float4 *dst = reinterpret_cast<float4 *>(s_acc + (wave * ROWS + row) * D + blk * kQK);
+    for (int e = 0; e < 32; ++e) acc[e] = __builtin_fmaf(acc[e], e < 16 ? f : f_hi, c8);
+    // Sum the four 16-lane rows without LDS: v_permlane32_swap on element
+    // pairs (2i, 2i+1) leaves rows 0-1 with element 2i and rows 2-3 with
+    // 2i+1, each summed over rows {r, r+2}; v_permlane16_swap on the pairs of
+    // those leaves row r with element 4j + {0, 2, 1, 3}[r] summed over all
+    // four rows.  Then the lanes of a row that own the same block are summed.
+    float z[16];
 #pragma unroll
-        for (int c = 0; c < 8; ++c)
-            dst[c] = make_float4(acc[4 * c], acc[4 * c + 1], acc[4 * c + 2], acc[4 * c + 3]);
+    for (int i = 0; i < 16; ++i) {
+        z[i] = swap_sum32(acc[2 * i], acc[2 * i + 1]);
     }
-    if constexpr (NW > 1) {
+    float ws[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        ws[j] = row_block_sum<LPK>(swap_sum16(z[2 * j], z[2 * j + 1]));
+    }
+    // Lane l (row r = l / 16) now holds elements blk * 32 + 4 j + mr, j < 8,
+    // mr = {0, 2, 1, 3}[r], replicated over the REP = 16 / LPK lanes of its
+    // row that own block blk; replica ri keeps j = jj * REP + ri, jj < 8 / REP,
+    // so each of the 8 / REP stores below has all 64 lanes writing distinct
+    // elements and together they cover the D outputs.
+    constexpr int REP = 16 / LPK;
+    constexpr int NJ = 8 / REP;
+    static_assert(REP <= 8 && NJ * REP == 8, "head_dim 64 or 128");
+    const int row = lane >> 4;
+    const int mr = (row & 1) * 2 + (row >> 1);
+    const int ri = (lane & 15) / LPK;
+    float o[NJ];
+#pragma unroll
+    for (int jj = 0; jj < NJ; ++jj) {
+        float v = ws[jj * REP];
+#pragma unroll
+        for (int r = 1; r < REP; ++r) v = (ri == r) ? ws[jj * REP + r] : v;
+        o[jj] = v;
+    }
+    const int obase = blk * kQK + 4 * ri + mr;  // element of o[jj] is obase + 4 REP jj
+    float L = l_wave;  // 2^24 times the weight sum of the whole window
+    if constexpr (NW == 1) {
+        const float inv_l = (L > 0.0f) ? 16777216.0f / L : 0.0f;
+#pragma unroll
+        for (int jj = 0; jj < NJ; ++jj) out_row[obase + 4 * REP * jj] = o[jj] * inv_l;
+    } else {
+        // Merge the waves: each writes its row of sums and its (max, sum).
+#pragma unroll
+        for (int jj = 0; jj < NJ; ++jj) s_acc[wave * D + obase + 4 * REP * jj] = o[jj];
         if (lane == 0) {
             s_m[wave] = m_wave;
             s_l[wave] = l_wave;
         }
-    }
-    __syncthreads();
-
-    // Merge waves and rows; a workgroup may have fewer threads than head_dim.
-    float fw[NW];
-    float L = l_wave;  // sum of weights of the whole window
-    if constexpr (NW > 1) {
+        __syncthreads();
         float M = s_m[0];
 #pragma unroll
         for (int w = 1; w < NW; ++w) M = fmaxf(M, s_m[w]);
+        float fw[NW];
         L = 0.0f;
 #pragma unroll
         for (int w = 0; w < NW; ++w) {
             fw[w] = __builtin_amdgcn_exp2f(s_m[w] - M);
             L = __builtin_fmaf(fw[w], s_l[w], L);
         }
-    } else {
-        fw[0] = 1.0f;
-    }
-    // Thread t sums the rows of waves w = t / D (mod the number of row
-    // groups) for output t % D; row groups beyond the first add through LDS.
-    constexpr int TPB = 64 * NW;
-    constexpr int NPART = TPB >= D ? TPB / D : 1;       // partial sums per output
-    constexpr int WPP = (NW + NPART - 1) / NPART;       // waves per partial
-    constexpr int PER_T = TPB >= D ? 1 : D / TPB;       // outputs per thread
-    float part[PER_T];
-#pragma unroll
-    for (int j = 0; j < PER_T; ++j) {
-        const int o = (threadIdx.x + j * TPB) % D;
-        const int pp = TPB >= D ? threadIdx.x / D : 0;
-        float a = 0.0f;
-#pragma unroll
-        for (int ww = 0; ww < WPP; ++ww) {
-            const int w = pp * WPP + ww;
-            if (w < NW) {
-                float r = 0.0f;
-#pragma unroll
-                for (int rr = 0; rr < ROWS; ++rr) r += s_acc[(w * ROWS + rr) * D + o];
-                a = __builtin_fmaf(fw[w], r, a);
-            }
-        }
-        part[j] = a;
-    }
-    const float inv_l = (L > 0.0f) ? 16777216.0f / L : 0.0f;  // L is 2^24 times the weight sum
-    if constexpr (NPART == 1) {
-#pragma unroll
-        for (int j = 0; j < PER_T; ++j) out_row[threadIdx.x + j * TPB] = part[0 + j] * inv_l;
-    } else {
-        __syncthreads();  // every thread has read s_acc; reuse it for the partials
-        s_acc[threadIdx.x] = part[0];
-        __syncthreads();
+        const float inv_l = (L > 0.0f) ? 16777216.0f / L : 0.0f;
         if (threadIdx.x < D) {
             float a = 0.0f;
 #pragma unroll
-            for (int pp = 0; pp < NPART; ++pp) a += s_acc[pp * D + threadIdx.x];
+            for (int w = 0; w < NW; ++w) a = __builtin_fmaf(fw[w], s_acc[w * D + threadIdx.x], a);
             out_row[threadIdx.x] = a * inv_l;
         }
     }
