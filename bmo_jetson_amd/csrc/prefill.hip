@@ -596,6 +596,13 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
         // A ring tile's keys must also precede pos0 (its last tile may reach
         // into the chunk's positions, which the chunk tiles supply).
         const bool whole = t0 + kTK - 1 <= (ring_t ? pos0 - 1 : pos0 + wq0) && t0 > w_hi - n_ctx;
+        // the lane's 8 scores as scalars: masking and the rescale shift then
+        // update them in place on both paths
+        float sv[QB][8];
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+            for (int k = 0; k < 8; ++k) sv[qb][k] = s[qb][k >> 2][k & 3];
         if (!whole) {
 #pragma unroll
             for (int qb = 0; qb < QB; ++qb) {
@@ -610,7 +617,7 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
                     for (int v = 0; v < 4; ++v) {
                         const int kk = sub * 16 + v;
                         const bool ok = kk <= rel_hi && kk > rel - n_ctx;
-                        s[qb][sub][v] = ok ? s[qb][sub][v] : -INFINITY;
+                        sv[qb][sub * 4 + v] = ok ? sv[qb][sub * 4 + v] : -INFINITY;
                     }
             }
         }
@@ -621,9 +628,8 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
             // max; the exact per-query maximum (a cross-lane reduction) is
             // only needed when some score exceeds the running max by
             // kRescale.
-            float tmax = vmax(vmax(vmax(s[qb][0][0], s[qb][0][1]), s[qb][0][2]),
-                              vmax(vmax(vmax(s[qb][0][3], s[qb][1][0]), s[qb][1][1]),
-                                   vmax(vmax(s[qb][1][2], s[qb][1][3]), -INFINITY)));
+            float tmax = vmax(vmax(vmax(sv[qb][0], sv[qb][1]), sv[qb][2]),
+                              vmax(vmax(vmax(sv[qb][3], sv[qb][4]), sv[qb][5]), vmax(sv[qb][6], sv[qb][7])));
             if (__any(tmax > dl[qb] + kRescale)) {
                 tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
                 tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
@@ -635,7 +641,7 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
                 dl[qb] = need ? 0.0f : dl[qb];
                 cneg[qb] -= shift;
 #pragma unroll
-                for (int sub = 0; sub < 2; ++sub) s[qb][sub] -= shift;
+                for (int k = 0; k < 8; ++k) sv[qb][k] -= shift;
                 // acc rows are queries 4c + v: fetch their alphas from lanes 4c + v
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
@@ -649,7 +655,7 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
             for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
                 for (int v = 0; v < 4; ++v)
-                    pop[qb][sub * 4 + v] = (_Float16) __builtin_amdgcn_exp2f(s[qb][sub][v]);
+                    pop[qb][sub * 4 + v] = (_Float16) __builtin_amdgcn_exp2f(sv[qb][sub * 4 + v]);
             accl[qb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pop[qb], ones, accl[qb], 0, 0, 0);
         }
         // O += P V: B operand lane l = column t*16 + n of the tile, keys
@@ -773,7 +779,7 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
         for (int v = 0; v < 4; ++v) {
             const float lv = accl[qb][v];
             const int qv = wq0 + qb * 16 + 4 * c + v;
-            const float inv = lv > 0.0f ? 1.0f / lv : 0.0f;
+            const float inv = lv > 0.0f ? __builtin_amdgcn_rcpf(lv) : 0.0f;  // within 1 ulp
             float *orow = p.out + (((int64_t) b * p.n_tok + min(qv, p.n_tok - 1)) * p.n_heads + h) * D;
 #pragma unroll
             for (int g = 0; g < NT / 4; ++g) {
