@@ -259,9 +259,15 @@ void *bmo_kv_ring_v_base(bmo_kv_ring_t *r) { return r ? r->mem + bmo::kVCodeOff 
 
 const char *bmo_kv_ring_last_error(const bmo_kv_ring_t *r) {
     if (!r) return t_create_error.empty() ? nullptr : t_create_error.c_str();
+    // a copy per thread: another thread's call on the ring may replace the
+    // ring's message while the caller still reads this one
+    thread_local std::string t_copy;
     auto *m = const_cast<bmo_kv_ring_t *>(r);
-    std::lock_guard<std::mutex> lk(m->mu);
-    return m->last_error.empty() ? nullptr : m->last_error.c_str();
+    {
+        std::lock_guard<std::mutex> lk(m->mu);
+        t_copy = m->last_error;
+    }
+    return t_copy.empty() ? nullptr : t_copy.c_str();
 }
 
 int bmo_kv_ring_reset(bmo_kv_ring_t *r, int session, void *stream) {

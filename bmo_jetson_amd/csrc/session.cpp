@@ -306,8 +306,13 @@ int bmo_attn_session_replay(bmo_attn_session_t *s, int pos) {
 
 const char *bmo_attn_session_last_error(bmo_attn_session_t *s) {
     if (!s) return t_session_create_error.empty() ? nullptr : t_session_create_error.c_str();
-    std::lock_guard<std::mutex> lk(s->mu);
-    return s->last_error.empty() ? nullptr : s->last_error.c_str();
+    // a copy per thread (see bmo_kv_ring_last_error)
+    thread_local std::string t_copy;
+    {
+        std::lock_guard<std::mutex> lk(s->mu);
+        t_copy = s->last_error;
+    }
+    return t_copy.empty() ? nullptr : t_copy.c_str();
 }
 
 }  // extern "C"

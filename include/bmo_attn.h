@@ -110,8 +110,8 @@ BMO_ATTN_API int bmo_kv_ring_reset(bmo_kv_ring_t *ring, int session,
 
 /* Message for the most recent failed call on ring, or for the calling
  * thread's last failed bmo_kv_ring_create when ring is NULL.  NULL if none.
- * Owned by the library, valid until the next call on the same ring/thread
- * (src/bmo_api.h:142-145). */
+ * Owned by the library (a per-thread copy), valid until this thread's next
+ * call of bmo_kv_ring_last_error (src/bmo_api.h:142-145). */
 BMO_ATTN_API const char *bmo_kv_ring_last_error(const bmo_kv_ring_t *ring);
 
 /* ---- decode path ------------------------------------------------------------ */
@@ -349,8 +349,9 @@ BMO_ATTN_API int bmo_attn_session_has_graph(bmo_attn_session_t *s);
 BMO_ATTN_API int bmo_attn_session_replay(bmo_attn_session_t *s, int pos);
 
 /* Message of the handle's most recent failed call, or (s == NULL) of the
- * calling thread's last failed create; NULL if none.  Owned by the library,
- * valid until the next call on the handle (src/bmo_api.h:142-145). */
+ * calling thread's last failed create; NULL if none.  Owned by the library
+ * (a per-thread copy), valid until this thread's next call of
+ * bmo_attn_session_last_error (src/bmo_api.h:142-145). */
 BMO_ATTN_API const char *bmo_attn_session_last_error(bmo_attn_session_t *s);
 
 /* ---- Q4_0 weight GEMV (the projections around attention) -------------------- */
