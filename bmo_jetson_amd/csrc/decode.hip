@@ -671,12 +671,13 @@ struct Shape {
 // for about 512 waves in all.  Below 128 units, 8 waves per unit (B=1, 32
 // units, over a 32-layer model step whose windows come from HBM: 6.86 us
 // plain and 7.03 us fused per layer, against 7.44 and 8.16 us with 4 waves;
-// fused, wave 0 takes the new token).  BMO_ATTN_SHAPE = "nw,pf" overrides
-// the choice (tuning; unknown shapes fall back to the default).
+// fused, wave 0 takes the new token), with two groups in flight per wave
+// when plain (5.62 against 5.74 us per layer with one) and one when fused
+// (5.87 against 5.89 us with two).  BMO_ATTN_SHAPE = "nw,pf" overrides the
+// choice (tuning; unknown shapes fall back to the default).
 Shape pick_shape(int64_t units, int n_groups, bool fused) {
-    (void) fused;
     Shape s{1, 2};
-    if (units < 128) s = Shape{8, 1};
+    if (units < 128) s = Shape{8, fused ? 1 : 2};
     else if (units < 256) s = Shape{4, 1};
     else if (units < 512) s = Shape{2, 1};
     while (s.nw > 1 && s.nw > n_groups) s.nw /= 2;  // no more waves than groups
