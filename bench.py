@@ -550,7 +550,8 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=300,
+                    help="untimed graph replays right before the timed region (300 cfg3 steps: about 0.25 s)")
     ap.add_argument("--config", default="cfg3", choices=["cfg3", "cfg4"])
     ap.add_argument("--sessions", type=int, default=None, help="override S (testing)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
