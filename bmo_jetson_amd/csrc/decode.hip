@@ -13,10 +13,10 @@
 // Work decomposition (gfx950, wave64).  A workgroup of NW waves serves one
 // (batch entry, query head) unit; its waves take contiguous pieces of the
 // window.  Batches with many units use one wave per unit; small batches (B=1
-// decode) use up to 16 waves per unit so that enough waves run, merging in LDS
-// (a split across workgroups would have to merge through device-scope
-// atomics, which serialize across the XCDs).  The ring stores slots in groups
-// of G = 64 / LPK keys
+// decode) use 2 to 8 waves per unit (16 on request) so that enough waves run,
+// merging in LDS (a split across workgroups would have to merge through
+// device-scope atomics, which serialize across the XCDs).  The ring stores
+// slots in groups of G = 64 / LPK keys
 // (ring_layout.hpp), LPK = head_dim / 32 blocks per key, so one group is one
 // wave iteration: lane l owns block l % LPK of key l / LPK and fetches its 16
 // K code bytes, 16 V code bytes and its (K, V) scale dword with three

@@ -218,8 +218,9 @@ __global__ __launch_bounds__(256) void commit_kernel(PrefillParams p) {
         *reinterpret_cast<const uint32_t *>(src + p.sg.scale_offset(i, blk));
 }
 
-// Eight waves per CU (two waves per SIMD): the register budget that keeps
-// the accumulators in architectural registers without spilling.
+// Launch bounds: 64 * QW threads, one workgroup per CU (QW = 16: four waves
+// per SIMD, at most 128 VGPRs each, which holds the accumulators, the query
+// operands and the fetched tile bytes without spilling).
 //
 // DIRECT: every (entry, kv head) stripe is read by this one workgroup (one
 // query head per kv head, the whole chunk in one workgroup).  The workgroup
