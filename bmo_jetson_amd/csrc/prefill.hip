@@ -13,8 +13,9 @@
 // The chunk overwrites slots that its own early queries still read (query 0
 // needs positions back to pos0 - n_ctx + 1).  With one query head per kv
 // head and at most 256 tokens, one workgroup reads each ring stripe: it
-// quantizes the chunk into LDS, attends, and writes the chunk's blocks into
-// the ring after its last tile (one kernel).  Otherwise one call runs three
+// quantizes the chunk into LDS, attends, and writes each chunk block into
+// the ring once the ring tile holding the slot's old position has been
+// dequantized (one kernel).  Otherwise one call runs three
 // kernels in stream order:
 //   stage_kernel   quantizes the chunk's bf16 K/V into a staging stripe with
 //                  the ring's group layout (slot i = chunk token i);
@@ -226,8 +227,8 @@ __global__ __launch_bounds__(256) void commit_kernel(PrefillParams p) {
 // query head per kv head, the whole chunk in one workgroup).  The workgroup
 // then quantizes its chunk's K/V itself into LDS (the staging stripe's role),
 // reads the chunk's keys from there, and writes the chunk's blocks into the
-// ring after its last tile, when no wave reads the old slots any more; no
-// stage or commit kernel runs.
+// ring during the tile loop, each once no wave reads its slot's old contents
+// from memory any more; no stage or commit kernel runs.
 template <int D, int QW, int QB, bool DIRECT, bool ALIGNED>
 __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams p) {
     constexpr int NBLK = D / kQK;
@@ -715,6 +716,40 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
     // a tile pair follows every wave's multiplication of the pair before, so
     // writing a buffer NBUF positions later is safe.
     if constexpr (DIRECT) quantize_chunk();
+    // DIRECT: the chunk's blocks go into their ring slots (pos0 + i) % n_ctx
+    // while the tiles are multiplied.  Chunk key i replaces old position
+    // pos0 + i - n_ctx, which only its ring tile carries (a 17th ring tile,
+    // sharing slots with the first, is live only at slots of positions below
+    // pos0 - n_ctx), and every wave reads that tile from LDS once it is
+    // deposited; the processing order visits the ring tiles in increasing
+    // order.  So once the ring tiles below r_done are published, keys whose
+    // old position precedes r_start + 32 r_done can be written.  The waves
+    // without dequantization items write them right after each barrier:
+    // they issue no global loads in the loop, so the stores delay no wait.
+    // No other workgroup reads this stripe.  (Loads of padding tiles read
+    // group 0 and may see new blocks; their values are never used.)
+    static_assert(!DIRECT || IPT == 1, "non-loading threads are those past the items");
+    constexpr int NL_FIRST = DIRECT ? ITEMS : 0;  // first thread without items
+    uint8_t *const wring = p.base + p.g.stripe_offset(p.layer, sid, kvh);
+    int i_done = 0;  // chunk keys written (wave-uniform, non-loading waves)
+    auto commit_until = [&](int lim) {
+        for (int e = (int) threadIdx.x - NL_FIRST + i_done * NBLK; e < lim * NBLK; e += NTHR - NL_FIRST) {
+            const int bb = e % NBLK;
+            const int i = e / NBLK;
+            const int slot = (pos0 + i) % n_ctx;
+            *reinterpret_cast<uint4 *>(wring + p.g.kcode_offset(slot, bb)) = sCc[i * NBLK + bb];
+            *reinterpret_cast<uint4 *>(wring + p.g.vcode_offset(slot, bb)) = sCc[(QT + i) * NBLK + bb];
+            *reinterpret_cast<uint32_t *>(wring + p.g.scale_offset(slot, bb)) = sCs[i * NBLK + bb];
+        }
+        i_done = max(i_done, lim);
+    };
+    // keys writable once the positions below P are published: ring tiles
+    // among them (the paired part's even positions, then the rest's first
+    // n_rt - n_pair), and keys whose old position precedes their end
+    auto commit_limit = [&](int P) {
+        const int r_done = P <= 2 * n_pair ? (P + 1) / 2 : n_pair + min(P - 2 * n_pair, n_rt - n_pair);
+        return min(p.n_tok, max(0, (r_start - pos0) + kTK * r_done + n_ctx));
+    };
     // The loop in two copies, so that the loading copy has its loads on
     // every path and the compiler's waits count exactly (loads behind a
     // branch turn every wait into a wait for all loads).
@@ -738,6 +773,10 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
                     }
                 }
                 lds_barrier();  // these TPB buffers are complete
+                if constexpr (DIRECT && !LOADS) {
+                    const int lim = commit_limit(base + u + TPB);
+                    if (lim > i_done) commit_until(lim);
+                }
 #pragma unroll
                 for (int k = 0; k < TPB; ++k) compute((u + k) % NBUF, tile_of(base + u + k));
             }
@@ -747,24 +786,10 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
         tile_loop(BoolC<true>{});
     else
         tile_loop(BoolC<false>{});
-
-    if constexpr (DIRECT) {
-        // The chunk's blocks into their ring slots (pos0 + i) % n_ctx.  Every
-        // wave of this workgroup has passed the last tile's barrier, which
-        // follows the last dequantization of ring data, so no wave still
-        // needs an old slot; no other workgroup reads this stripe.  (Loads
-        // of the padding tiles past the end may still be in flight; their
-        // values are never used.)
-        uint8_t *wring = p.base + p.g.stripe_offset(p.layer, sid, kvh);
-        for (int e = threadIdx.x; e < p.n_tok * NBLK; e += NTHR) {
-            const int bb = e % NBLK;
-            const int i = e / NBLK;
-            const int slot = (pos0 + i) % n_ctx;
-            *reinterpret_cast<uint4 *>(wring + p.g.kcode_offset(slot, bb)) = sCc[i * NBLK + bb];
-            *reinterpret_cast<uint4 *>(wring + p.g.vcode_offset(slot, bb)) = sCc[(QT + i) * NBLK + bb];
-            *reinterpret_cast<uint32_t *>(wring + p.g.scale_offset(slot, bb)) = sCs[i * NBLK + bb];
-        }
-    }
+    // (the last barrier publishes every ring tile, so the loop has written
+    // every key; this covers nothing unless n_tiles is 0)
+    if constexpr (DIRECT)
+        if (!has_items) commit_until(p.n_tok);
 
     // Every acc row (query 4c + v) divides by its weight sum.  Lane 4qd + j
     // (of the 16 sharing c) holds, for column tile t, element
