@@ -54,6 +54,13 @@ typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
+// Reads an int at a wave-uniform index through the scalar cache.  For
+// arrays that no kernel writes while the reading kernel runs (session ids,
+// positions), so the constant address space is exact.
+__device__ __forceinline__ int load_scalar_i32(const int *ptr, int i) {
+    return ((const __attribute__((address_space(4))) int *) ptr)[i];
+}
+
 template <bool B>
 struct BoolC {
     static constexpr bool value = B;
@@ -267,17 +274,24 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
     // wave-uniform (readfirstlane), so that everything derived from it --
     // the tile skip, the whole-tile test -- is a scalar branch
     const int wave = __builtin_amdgcn_readfirstlane((int) threadIdx.x >> 6);
+    // (scalars: the divisions run on the vector unit, readfirstlane keeps
+    // their results, and the addresses derived from them, in SGPRs)
     const int n_qt = (p.n_tok + QT - 1) / QT;
-    const int qt = blockIdx.x % n_qt;
-    const int unit = blockIdx.x / n_qt;
-    const int b = unit / p.n_heads;
+    const int unit = __builtin_amdgcn_readfirstlane((int) blockIdx.x / n_qt);
+    const int qt = (int) blockIdx.x - unit * n_qt;
+    const int b = __builtin_amdgcn_readfirstlane(unit / p.n_heads);
     const int h = unit - b * p.n_heads;
     const int i0 = qt * QT;
     const int q_per_kv = p.n_heads / p.n_kv;
-    const int kvh = h / q_per_kv;
+    const int kvh = __builtin_amdgcn_readfirstlane(h / q_per_kv);
 
-    const int sid = p.session_ids ? p.session_ids[b] : b;
-    const int pos0 = p.pos0[b];
+    // Scalar loads: as vector loads they returned only after the loads that
+    // the workgroup's other waves had issued before them (up to 5 us for the
+    // last wave at cfg5, measured), and that wave's own loads waited for
+    // them.  (The call's time at cfg5 is the same either way: there the
+    // prologue's loads are bandwidth-bound.)
+    const int sid = p.session_ids ? load_scalar_i32(p.session_ids, b) : b;
+    const int pos0 = load_scalar_i32(p.pos0, b);
     const int nq = min(QT, p.n_tok - i0);  // valid queries of this workgroup
     if (sid < 0 || sid >= p.g.n_sessions || pos0 < 0 || pos0 > INT_MAX - p.n_tok) {
         for (int e = threadIdx.x; e < nq * D; e += blockDim.x) {
