@@ -384,8 +384,10 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
     // chunk tiles, padding tiles past the end -- read the ring stripe's first
     // slots, which stay cached), so the number of loads in flight is the same
     // on every path and the compiler's waits stay exact.  Depth: 3 tiles
-    // with 16 waves (4 per SIMD hide the rest; 84.0 vs 85.7 us at depth 7,
-    // cfg5, and no register spills in any instantiation), 7 with fewer.
+    // with 16 waves (4 per SIMD hide the rest; at cfg5 depth 7 measured
+    // 85.7 vs 84.0 us in an earlier build and 78.4 vs 74.2 us in this one,
+    // where it spills 3 VGPRs; depth 3 spills in no instantiation), 7 with
+    // fewer.
     constexpr int PF = QW >= 16 ? 3 : 7;
     static_assert((PF + 1) % NBUF == 0, "the unrolled slot must determine the LDS buffer");
     uint2 raw[PF + 1][IPT];
