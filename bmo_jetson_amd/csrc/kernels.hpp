@@ -89,6 +89,7 @@ struct PrefillParams {
     const uint16_t *v;
     float *out;    // [n_batch][n_tok][n_heads][head_dim]
     float qscale;  // softmax scale * log2(e)
+    int n_resident;  // set by launch_prefill: workgroups the device runs at once (0: unknown)
 };
 
 // Launchers enqueue only; they leave launch errors for the caller's

@@ -766,6 +766,29 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
         const int r_done = P <= 2 * n_pair ? (P + 1) / 2 : n_pair + min(P - 2 * n_pair, n_rt - n_pair);
         return min(p.n_tok, max(0, (r_start - pos0) + kTK * r_done + n_ctx));
     };
+    // DIRECT: halfway through the loop the waves without items read one
+    // dword of every 128-byte line of the query rows of workgroup
+    // blockIdx.x + n_resident, the one the dispatcher is likely to start
+    // when a workgroup of this XCD finishes (workgroups go to the XCDs in
+    // turn, and this one's XCD is that one's).  Its query loads then hit this
+    // XCD's L2 (64 KB a workgroup, 2 MB an XCD at cfg5; the output's
+    // nontemporal stores leave the L2 to them).  A round's whole input does
+    // not fit the L2.  Measured at cfg5 with the output stores: 71.7 vs
+    // 72.5 us full history (74.2 without either), 46.7 vs 46.9 us empty.
+    const int succ = (int) blockIdx.x + p.n_resident;
+    const bool touch_on = DIRECT && p.n_resident > 0 && succ < (int) gridDim.x;
+    constexpr int LPR = D * 2 / 128;  // 128-byte lines of a query row
+    const int touch_at = ((n_tiles + PF) / (PF + 1)) * (PF + 1) / 2 & ~(TPB - 1);
+    uint32_t touched = 0;
+    auto touch_successor = [&]() {
+        const int su = succ / n_qt;
+        const int sb = su / p.n_heads;
+        const int sh = su - sb * p.n_heads;
+        const int t = (int) threadIdx.x - NL_FIRST;
+        const int row = min(t / LPR, p.n_tok - 1);
+        const uint16_t *line = p.q + (((int64_t) sb * p.n_tok + row) * p.n_heads + sh) * D + (t % LPR) * 64;
+        touched = *reinterpret_cast<const uint32_t *>(line);
+    };
     // The loop in two copies, so that the loading copy has its loads on
     // every path and the compiler's waits count exactly (loads behind a
     // branch turn every wait into a wait for all loads).
@@ -792,6 +815,7 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
                 if constexpr (DIRECT && !LOADS) {
                     const int lim = commit_limit(base + u + TPB);
                     if (lim > i_done) commit_until(lim);
+                    if (touch_on && base + u == touch_at) touch_successor();
                 }
 #pragma unroll
                 for (int k = 0; k < TPB; ++k) compute((u + k) % NBUF, tile_of(base + u + k));
@@ -802,6 +826,8 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
         tile_loop(BoolC<true>{});
     else
         tile_loop(BoolC<false>{});
+    // (the touched value is needed by nothing; the read must not be dropped)
+    asm volatile("" ::"v"(touched));
     // (the last barrier publishes every ring tile, so the loop has written
     // every key; this covers nothing unless n_tiles is 0)
     if constexpr (DIRECT)
@@ -843,7 +869,10 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
                 // c_k is element base + {0, 2, 1, 3}[k] of tile t = 4g + jq
                 const int t = 4 * g + jq;
                 const int base = 32 * (t >> 1) + 8 * (t & 1) + 4 * (qd >> 1) + 16 * (qd & 1);
-                if (qv < p.n_tok) *reinterpret_cast<float4 *>(orow + base) = make_float4(c0, c2, c1, c3);
+                // nontemporal: nothing here reads the output again, and it
+                // would displace the L2 lines the next workgroups load
+                if (qv < p.n_tok)
+                    __builtin_nontemporal_store(float4_t{c0, c2, c1, c3}, reinterpret_cast<float4_t *>(orow + base));
             }
         }
     }
@@ -881,6 +910,20 @@ void launch_attention(const PrefillParams &p, bool direct, dim3 grid, hipStream_
 
 }  // namespace
 
+// Workgroups of prefill_kernel that the current device runs at once: its
+// CU count (one workgroup fills a CU).  Looked up once per device.
+static int resident_workgroups() {
+    static int cached[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    if (cached[dev] <= 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) n = 0;
+        cached[dev] = n > 0 ? n : -1;
+    }
+    return cached[dev] > 0 ? cached[dev] : 0;
+}
+
 bool prefill_is_direct(const PrefillParams &p) { return p.n_heads == p.n_kv && p.n_tok <= kQT; }
 
 bool launch_prefill(const PrefillParams &p, hipStream_t stream) {
@@ -894,10 +937,12 @@ bool launch_prefill(const PrefillParams &p, hipStream_t stream) {
     }
     const int qt = kQT;
     const dim3 grid((unsigned) ((int64_t) p.n_batch * p.n_heads * ((p.n_tok + qt - 1) / qt)));
+    PrefillParams pa = p;
+    pa.n_resident = resident_workgroups();
     if (p.g.head_dim == 128)
-        launch_attention<128>(p, direct, grid, stream);
+        launch_attention<128>(pa, direct, grid, stream);
     else
-        launch_attention<64>(p, direct, grid, stream);
+        launch_attention<64>(pa, direct, grid, stream);
     if (!direct) {
         const int commit_threads = p.n_batch * p.n_tok * p.n_kv * nblk;
         hipLaunchKernelGGL(commit_kernel, dim3((unsigned) ((commit_threads + 255) / 256)), dim3(256), 0,
