@@ -766,19 +766,21 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
         const int r_done = P <= 2 * n_pair ? (P + 1) / 2 : n_pair + min(P - 2 * n_pair, n_rt - n_pair);
         return min(p.n_tok, max(0, (r_start - pos0) + kTK * r_done + n_ctx));
     };
-    // DIRECT: halfway through the loop the waves without items read one
-    // dword of every 128-byte line of the query rows of workgroup
-    // blockIdx.x + n_resident, the one the dispatcher is likely to start
-    // when a workgroup of this XCD finishes (workgroups go to the XCDs in
-    // turn, and this one's XCD is that one's).  Its query loads then hit this
-    // XCD's L2 (64 KB a workgroup, 2 MB an XCD at cfg5; the output's
+    // DIRECT: 8 tiles before the loop's end (4 barrier periods) the waves
+    // without items read one dword of every 128-byte line of the query rows
+    // of workgroup blockIdx.x + n_resident, the one the dispatcher is likely
+    // to start when a workgroup of this XCD finishes (workgroups go to the
+    // XCDs in turn, and this one's XCD is that one's).  Its query loads then
+    // hit this XCD's L2 (64 KB a workgroup, 2 MB an XCD at cfg5; the output's
     // nontemporal stores leave the L2 to them).  A round's whole input does
-    // not fit the L2.  Measured at cfg5 with the output stores: 71.7 vs
-    // 72.5 us full history (74.2 without either), 46.7 vs 46.9 us empty.
+    // not fit the L2, and touching the chunk's K rows too was slower (75.9
+    // vs 72.7 us).  At cfg5, against the same kernel without the touch and
+    // with plain output stores: 70.5 vs 73.2-74.2 us full history, 46.1 vs
+    // 47.0 us empty; halfway through the loop instead, 71.3-71.7 / 46.7-47.7.
     const int succ = (int) blockIdx.x + p.n_resident;
     const bool touch_on = DIRECT && p.n_resident > 0 && succ < (int) gridDim.x;
     constexpr int LPR = D * 2 / 128;  // 128-byte lines of a query row
-    const int touch_at = ((n_tiles + PF) / (PF + 1)) * (PF + 1) / 2 & ~(TPB - 1);
+    const int touch_at = max(0, (n_tiles + PF) / (PF + 1) * (PF + 1) - 8) & ~(TPB - 1);
     uint32_t touched = 0;
     auto touch_successor = [&]() {
         const int su = succ / n_qt;
