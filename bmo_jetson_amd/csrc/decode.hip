@@ -135,14 +135,16 @@ __device__ __forceinline__ float row_sum(float v) {
 // returned pair.  The instruction exchanges lanes 32-63 of a with lanes 0-31
 // of b (permlane32: a = {a rows 0-1, b rows 0-1}, b = {a rows 2-3, b rows
 // 2-3}) or the odd rows of a with the even rows of b (permlane16: a = {a r0,
-// b r0, a r2, b r2}, b = {a r1, b r1, a r3, b r3}).  The s_nop gives the two
-// wait states a swap needs after a VALU write of its operands.
+// b r0, a r2, b r2}, b = {a r1, b r1, a r3, b r3}).  The compiler's hazard
+// pass does not look inside inline asm, so the s_nop provides the wait
+// states itself: 4, which covers a VALU write of the operands (2 needed) and
+// a VALU write of EXEC (v_cmpx) right before the swap as well.
 __device__ __forceinline__ float swap_sum32(float a, float b) {
-    asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    asm("s_nop 3\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
     return a + b;
 }
 __device__ __forceinline__ float swap_sum16(float a, float b) {
-    asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    asm("s_nop 3\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
     return a + b;
 }
 __device__ __forceinline__ float lane_value(float v, int lane) {
@@ -665,6 +667,15 @@ struct Shape {
     int nw, pf;
 };
 
+// The shapes launch_shape instantiates.
+constexpr Shape kShapes[] = {{1, 1}, {1, 2}, {1, 3}, {2, 1}, {4, 1}, {8, 1}, {8, 2}, {16, 1}};
+
+constexpr bool shape_instantiated(Shape s) {
+    for (const Shape &k : kShapes)
+        if (k.nw == s.nw && k.pf == s.pf) return true;
+    return false;
+}
+
 // Workgroup shape per call: one wave per (entry, head) unit with two groups
 // of loads in flight when there are enough units to fill the chip (measured
 // best over sustained runs of BASELINE config 3), else enough waves per unit
@@ -673,14 +684,33 @@ struct Shape {
 // plain and 7.03 us fused per layer, against 7.44 and 8.16 us with 4 waves;
 // fused, wave 0 takes the new token), with two groups in flight per wave
 // when plain (5.62 against 5.74 us per layer with one) and one when fused
-// (5.87 against 5.89 us with two).  BMO_ATTN_SHAPE = "nw,pf" overrides the
-// choice (tuning; unknown shapes fall back to the default).
-Shape pick_shape(int64_t units, int n_groups, bool fused) {
+// (5.87 against 5.89 us with two).  A window of fewer groups than waves
+// halves the waves, with one group in flight below 8 waves.
+constexpr Shape default_shape(int64_t units, int n_groups, bool fused) {
     Shape s{1, 2};
     if (units < 128) s = Shape{8, fused ? 1 : 2};
     else if (units < 256) s = Shape{4, 1};
     else if (units < 512) s = Shape{2, 1};
-    while (s.nw > 1 && s.nw > n_groups) s.nw /= 2;  // no more waves than groups
+    while (s.nw > 1 && s.nw > n_groups) {  // no more waves than groups
+        s.nw /= 2;
+        s.pf = 1;
+    }
+    return s;
+}
+
+constexpr bool default_shapes_instantiated() {
+    for (int64_t units : {1, 32, 127, 128, 255, 256, 511, 512, 1 << 20})
+        for (int n_groups = 1; n_groups <= 64; ++n_groups)
+            for (bool fused : {false, true})
+                if (!shape_instantiated(default_shape(units, n_groups, fused))) return false;
+    return true;
+}
+static_assert(default_shapes_instantiated(), "every default decode shape has a kernel");
+
+// BMO_ATTN_SHAPE = "nw,pf" overrides the default (tuning); a shape without a
+// kernel falls back to one wave with one group in flight.
+Shape pick_shape(int64_t units, int n_groups, bool fused) {
+    Shape s = default_shape(units, n_groups, fused);
     if (const char *e = std::getenv("BMO_ATTN_SHAPE")) {
         Shape o{0, 0};
         if (std::sscanf(e, "%d,%d", &o.nw, &o.pf) == 2) s = o;
@@ -691,6 +721,7 @@ Shape pick_shape(int64_t units, int n_groups, bool fused) {
 template <int D>
 bool launch_shape(const DecodeParams &p, bool fused, hipStream_t stream, const Shape &s) {
 #define BMO_SHAPE(NW_, PF_)                                \
+    static_assert(shape_instantiated(Shape{NW_, PF_}));    \
     if (s.nw == NW_ && s.pf == PF_) {                      \
         launch_variant<D, NW_, PF_>(p, fused, stream);     \
         return true;                                       \
@@ -704,6 +735,7 @@ bool launch_shape(const DecodeParams &p, bool fused, hipStream_t stream, const S
     BMO_SHAPE(8, 2)
     BMO_SHAPE(16, 1)
 #undef BMO_SHAPE
+    static_assert(sizeof(kShapes) / sizeof(kShapes[0]) == 8, "kShapes lists the shapes dispatched above");
     return false;
 }
 

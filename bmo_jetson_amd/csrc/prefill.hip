@@ -27,18 +27,23 @@
 // reads from LDS feeds QB matrix instructions.  Keys stream through four LDS
 // buffers in tiles of 32 positions: each thread of the loading waves holds
 // its share of the Q4_0 bytes of the next tiles in registers and
-// dequantizes the oldest two into free buffers (K and V row-major) as the
-// fp16 value (code - 8) * d; one barrier publishes each pair of tiles.  A
-// wave skips tiles that hold no key its queries may see, and the tiles are
-// paired so that, where the causal and window masks allow, the two tiles of
-// a pair are seen by different waves.  Each wave computes S^T = K Q^T with
-// v_mfma_f32_16x16x32_f16 (the D layout of S^T puts 8 keys of one query in a
-// lane, exactly the A layout the P.V product needs), runs an online softmax
-// in the log2 domain and accumulates O += P V with the same instruction, its
-// V operand read from the row-major tile with ds_read_b64_tr_b16.
-// Operands: q (bf16 inputs, scaled by scale*log2 e) and the dequantized K, V
-// and the weights P in fp16, accumulation in fp32.  K and V values fit fp16
-// as the reference's F16 cache requires.
+// dequantizes the oldest two into free buffers (K and V row-major); one
+// barrier publishes each pair of tiles.  A wave skips tiles that hold no key
+// its queries may see, and the tiles are paired so that, where the causal
+// and window masks allow, the two tiles of a pair are seen by different
+// waves.  Each wave computes S^T = K Q^T with v_mfma_f32_16x16x32_f16 (the D
+// layout of S^T puts 8 keys of one query in a lane, exactly the A layout the
+// P.V product needs), runs an online softmax in the log2 domain and
+// accumulates O += P V with the same instruction, its V operand read from
+// the row-major tile with ds_read_b64_tr_b16.
+// Precision.  The scores are as close as fp32 arithmetic on the bf16 q and
+// the dequantized K: K enters the matrix cores as its codes (c - 8), exact
+// in fp16, one product per 32-element block, and each block's fp16 scale d
+// multiplies that product in fp32; q enters as q * 2^e, exact in fp16, with
+// e chosen per query row, and scale * log2(e) * 2^-e multiplies the fp32
+// score.  V enters as the fp16 value (c - 8) * d and the weights P as fp16,
+// accumulation in fp32.  V values fit fp16 as the reference's F16 cache
+// requires.
 #include <limits.h>
 #include <math.h>
 
@@ -116,6 +121,11 @@ __host__ __device__ constexpr int col_elem(int s) {
     return (s & ~31) + 4 * ((s & 31) >> 3) + perm_elem(s & 7);
 }
 
+// Place of key k's block scale within a block's 32 entries: keys 4c + v and
+// 16 + 4c + v (v = 0..3) at 8c + v and 8c + 4 + v, the order in which lane
+// group c holds the scores of its keys in the two S^T products of a tile.
+__host__ __device__ constexpr int kd_slot(int k) { return 8 * ((k >> 2) & 3) + 4 * (k >> 4) + (k & 3); }
+
 // The output store's float4 layout: lane 4qd + j of a 16-lane group holds
 // column slot 16t + 4qd + j, element base(qd, t) + {0, 2, 1, 3}[j].
 __host__ __device__ constexpr bool store_layout_matches() {
@@ -141,6 +151,8 @@ constexpr uint32_t kXorLoV = 0x64006400u, kXorHiV = 0x54005400u;
 // (n << 4) under 0x5400, reads 64 + n, so no shift per nibble is needed.
 // xlo/xhi are those patterns, K's with the stored bit 3 flipped back (the xor
 // touches only nibble bits and the pattern's own, disjoint bits).
+// SCALED false: the codes alone, (code - 8) exactly (d16 unused).
+template <bool SCALED = true>
 __device__ __forceinline__ half8_t dequant_dword(uint32_t w, uint32_t d16, uint32_t xlo, uint32_t xhi) {
     const half2_t off_lo = {(_Float16) -1032.0f, (_Float16) -1032.0f};
     const half2_t off_hi = {(_Float16) -72.0f, (_Float16) -72.0f};
@@ -148,10 +160,14 @@ __device__ __forceinline__ half8_t dequant_dword(uint32_t w, uint32_t d16, uint3
     const half2_t dd = {d, d};
     const uint32_t y = w >> 8;
     half2_t r[4];
-    r[0] = (__builtin_bit_cast(half2_t, (w & 0x000F000Fu) ^ xlo) + off_lo) * dd;
-    r[1] = (__builtin_bit_cast(half2_t, (y & 0x000F000Fu) ^ xlo) + off_lo) * dd;
-    r[2] = (__builtin_bit_cast(half2_t, (w & 0x00F000F0u) ^ xhi) + off_hi) * dd;
-    r[3] = (__builtin_bit_cast(half2_t, (y & 0x00F000F0u) ^ xhi) + off_hi) * dd;
+    r[0] = __builtin_bit_cast(half2_t, (w & 0x000F000Fu) ^ xlo) + off_lo;
+    r[1] = __builtin_bit_cast(half2_t, (y & 0x000F000Fu) ^ xlo) + off_lo;
+    r[2] = __builtin_bit_cast(half2_t, (w & 0x00F000F0u) ^ xhi) + off_hi;
+    r[3] = __builtin_bit_cast(half2_t, (y & 0x00F000F0u) ^ xhi) + off_hi;
+    if constexpr (SCALED) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r[i] *= dd;
+    }
     // r[0] = (e0, e2), r[1] = (e1, e3), r[2] = (e16, e18), r[3] = (e17, e19)
     half8_t o;
     o[0] = r[0].x;
@@ -238,6 +254,7 @@ __global__ __launch_bounds__(256) void commit_kernel(PrefillParams p) {
 // from memory any more; no stage or commit kernel runs.
 template <int D, int QW, int QB, bool DIRECT, bool ALIGNED>
 __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams p) {
+    static_assert(!DIRECT || ALIGNED, "the direct path serves rings of a multiple of 32 slots");
     constexpr int NBLK = D / kQK;
     // LDS rows (fp16) of D + 16 halves, K and V alike: with that stride the
     // K operand reads (ds_read_b128: lane l reads a 16-byte chunk of key
@@ -262,9 +279,24 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
     // workgroup synchronize once per TPB tiles.
     constexpr int TPB = 2;
     constexpr int NBUF = 2 * TPB;
+    // Blocks whose S^T products are issued together (operands and scales
+    // read first): all of them on the direct path; two on the staged path,
+    // whose fetch holds more registers (four spill there).
+    constexpr int SB = DIRECT ? NBLK : (NBLK < 2 ? NBLK : 2);
+    static_assert(NBLK % SB == 0, "whole groups of blocks");
 
+    // K rows hold the codes (c - 8), exact in fp16, and sKd the blocks'
+    // fp16 scales d: element (key k, block bb) at bb * 32 + kd_slot(k), so
+    // that lane group c reads the scales of its keys 4c..4c+3 and
+    // 16+4c..16+4c+3 of a block as one 16-byte piece.  The scores then take
+    // (c - 8) . q per block from the matrix cores and the factor d in fp32:
+    // an fp16 (c - 8) * d would be rounded to 11 bits, an error that large
+    // query elements amplify past the tolerance.
     __shared__ __align__(16) _Float16 sK[NBUF][kTK * KROW];
+    __shared__ __align__(16) _Float16 sKd[NBUF][kTK * NBLK];
     __shared__ __align__(16) _Float16 sV[NBUF][kTK * VROW];
+    __shared__ __align__(16) _Float16 sOnes[8];  // B operand of the row-sum product
+    if (threadIdx.x < 8) sOnes[threadIdx.x] = (_Float16) 1.0f;  // (published by the loop's first barrier)
     // DIRECT: the chunk's blocks in ring format: codes [K/V][token][block]
     // (K as code ^ 8), scale dwords [token][block] (K low half, V high)
     __shared__ __align__(16) uint4 sCc[DIRECT ? 2 * QT * NBLK : 1];
@@ -464,14 +496,22 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
                 }
                 const uint32_t dw = it_v[j] ? sd >> 16 : sd;
                 const uint32_t d16 = live ? dw : 0u;
-                const uint32_t xlo = it_v[j] ? kXorLoV : kXorLoK;
-                const uint32_t xhi = it_v[j] ? kXorHiV : kXorHiK;
-                const half8_t v0 = dequant_dword(w.x, d16, xlo, xhi);
-                const half8_t v1 = dequant_dword(w.y, d16, xlo, xhi);
                 const int bb = (it >> 1) % NBLK;
                 const int hf = it & 1;
-                _Float16 *dst = it_v[j] ? &sV[buf][key * VROW + bb * kQK + 16 * hf]
-                                        : &sK[buf][key * KROW + bb * kQK + 16 * hf];
+                half8_t v0, v1;
+                _Float16 *dst;
+                if (it_v[j]) {  // (wave-uniform)
+                    v0 = dequant_dword(w.x, d16, kXorLoV, kXorHiV);
+                    v1 = dequant_dword(w.y, d16, kXorLoV, kXorHiV);
+                    dst = &sV[buf][key * VROW + bb * kQK + 16 * hf];
+                } else {
+                    v0 = dequant_dword<false>(w.x, 0u, kXorLoK, kXorHiK);
+                    v1 = dequant_dword<false>(w.y, 0u, kXorLoK, kXorHiK);
+                    dst = &sK[buf][key * KROW + bb * kQK + 16 * hf];
+                    // a dead key's scale is 0, so its (finite) block dot
+                    // products add nothing before the mask replaces them
+                    if (hf == 0) sKd[buf][bb * kTK + kd_slot(key)] = __builtin_bit_cast(_Float16, (uint16_t) d16);
+                }
                 *reinterpret_cast<half8_t *>(dst) = v0;
                 *reinterpret_cast<half8_t *>(dst + 8) = v1;
             }
@@ -538,10 +578,19 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
         }
         __builtin_amdgcn_sched_barrier(0);
     }
+    // Query operands: each row is scaled by the power of two 2^eq that puts
+    // its largest magnitude in [2^14, 2^15), so every bf16 element (8
+    // significant bits) is exact in fp16 down to 2^-31 of the row's maximum
+    // and no row overflows, whatever its range.  fq = scale * log2(e) *
+    // 2^-eq, applied to the fp32 scores, carries the rest of the factor.
+    // (A NaN or an infinity in a row makes that query's output NaN.)
     half8_t qop[QB][NBLK];
+    float fq[QB];
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
         const bool q_ok = wq0 + qb * 16 + n < p.n_tok;
+        float xq[NBLK][8];
+        float amax = 0.0f;
 #pragma unroll
         for (int bb = 0; bb < NBLK; ++bb) {
             // elements 4c + {0,1,2,3} in lo, 4c + 16 + {0,1,2,3} in hi; the
@@ -550,9 +599,20 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
             const uint32_t e[8] = {lo.x & 0xFFFFu, lo.y & 0xFFFFu, lo.x >> 16, lo.y >> 16,
                                    hi.x & 0xFFFFu, hi.y & 0xFFFFu, hi.x >> 16, hi.y >> 16};
 #pragma unroll
-            for (int r = 0; r < 8; ++r)
-                qop[qb][bb][r] = (_Float16) (q_ok ? bf16_to_f32(e[r]) * p.qscale : 0.0f);
+            for (int r = 0; r < 8; ++r) {
+                xq[bb][r] = q_ok ? bf16_to_f32(e[r]) : 0.0f;
+                amax = fmaxf(amax, fabsf(xq[bb][r]));
+            }
         }
+        // the row's other elements are in lanes n + 16, n + 32, n + 48
+        amax = fmaxf(amax, __shfl_xor(amax, 16));
+        amax = fmaxf(amax, __shfl_xor(amax, 32));
+        const int eq = 15 - __builtin_amdgcn_frexp_expf(amax);  // amax = m 2^ex, m in [0.5, 1)
+        fq[qb] = __builtin_amdgcn_ldexpf(p.qscale, -eq);
+#pragma unroll
+        for (int bb = 0; bb < NBLK; ++bb)
+#pragma unroll
+            for (int r = 0; r < 8; ++r) qop[qb][bb][r] = (_Float16) __builtin_amdgcn_ldexpf(xq[bb][r], eq);
     }
     // this wave's query positions and the keys they may see (wave-uniform)
     const int wq1 = min(wq0 + QWV - 1, p.n_tok - 1);
@@ -563,51 +623,67 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
     // times a ones operand, whose every column is the weight sum of a query
     // row; both use the D layout (lane l: column l % 16, queries 4c + v), so
     // the final division needs no cross-lane exchange.
-    // Softmax state per query block (log2 domain).  The S^T products start
-    // from -off, a per-query offset, so they come out as score - off; dl =
-    // running max - off.  off is 0 until a query's first rescale, which
-    // sets off to the running max (dl = 0) and is exact then because the
-    // products were taken from 0.  A rescale happens whenever a score
-    // exceeds the running max by kRescale, so after the test below every
-    // query with a finite score has dl = 0 and its weights are exp2 of the
-    // products themselves; a query still at the floor has only -inf scores,
-    // whose weights are 0 either way.
+    // Softmax state per query block (log2 domain).  A lane's scores are
+    // fq * (sum over blocks of d * (c - 8) . q') - off, one fma from the
+    // blocks' sum, with off a per-query offset; dl = running max - off.  off
+    // is 0 until a query's first rescale, which sets off to the running max
+    // (dl = 0) and is exact then because the scores were taken from 0.  A
+    // rescale happens whenever a score exceeds the running max by kRescale,
+    // so after the test below every query with a finite score has dl = 0
+    // and its weights are exp2 of the scores themselves; a query still at
+    // the floor has only -inf scores, whose weights are 0 either way.
     float dl[QB];
-    float4_t cneg[QB];  // -off for each of the lane's four products
+    float cneg[QB];  // -off
     float4_t acc[QB][NT];
     float4_t accl[QB];
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
         dl[qb] = kMaxFloor;
-        cneg[qb] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        cneg[qb] = 0.0f;
         accl[qb] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int t = 0; t < NT; ++t) acc[qb][t] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
     }
-    half8_t ones = {(_Float16) 1.0f, (_Float16) 1.0f, (_Float16) 1.0f, (_Float16) 1.0f,
-                    (_Float16) 1.0f, (_Float16) 1.0f, (_Float16) 1.0f, (_Float16) 1.0f};
-    // opaque to the compiler, so that it stays in registers instead of being
-    // rebuilt with three moves before every tile's row-sum product
-    asm volatile("" : "+v"(ones));
 
     auto compute = [&](int buf, int T) {
         const bool ring_t = T < n_rt;
         const int t0 = tile_t0(T);
         if (wq0 >= p.n_tok || t0 > w_hi || t0 + kTK - 1 < w_lo) return;  // nothing to see
         // S^T for keys 0..15 and 16..31 of the tile: lane l gets keys
-        // 4c + v (and 16 + 4c + v) of query n of each query block.
+        // 4c + v (and 16 + 4c + v) of query n of each query block.  One
+        // product per block over its 32 codes (exact integers times exact
+        // fp16 q'), scaled by the block's d in fp32.
+        const float4_t zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
         float4_t s[QB][2];
 #pragma unroll
         for (int sub = 0; sub < 2; ++sub) {
 #pragma unroll
-            for (int qb = 0; qb < QB; ++qb) s[qb][sub] = cneg[qb];
+            for (int b0 = 0; b0 < NBLK; b0 += SB) {
+                // SB blocks' operands and scales first, then their independent
+                // products, then the scaling: the products issue back to back
+                // instead of one LDS round trip each
+                half8_t kop[SB];
+                half4_t dv[SB];  // d of keys sub * 16 + 4c + v
 #pragma unroll
-            for (int bb = 0; bb < NBLK; ++bb) {
-                const half8_t kop = *reinterpret_cast<const half8_t *>(
-                    &sK[buf][(sub * 16 + n) * KROW + bb * kQK + 8 * c]);
+                for (int j = 0; j < SB; ++j) {
+                    const int bb = b0 + j;
+                    kop[j] = *reinterpret_cast<const half8_t *>(&sK[buf][(sub * 16 + n) * KROW + bb * kQK + 8 * c]);
+                    dv[j] = *reinterpret_cast<const half4_t *>(&sKd[buf][bb * kTK + 8 * c + 4 * sub]);
+                }
 #pragma unroll
-                for (int qb = 0; qb < QB; ++qb)
-                    s[qb][sub] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop, qop[qb][bb], s[qb][sub], 0, 0, 0);
+                for (int qb = 0; qb < QB; ++qb) {
+                    float4_t t[SB];
+#pragma unroll
+                    for (int j = 0; j < SB; ++j)
+                        t[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop[j], qop[qb][b0 + j], zero4, 0, 0, 0);
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        float a = b0 == 0 ? 0.0f : s[qb][sub][v];
+#pragma unroll
+                        for (int j = 0; j < SB; ++j) a = fmaf(t[j][v], (float) dv[j][v], a);
+                        s[qb][sub][v] = a;
+                    }
+                }
             }
         }
         // Mask (causal + window) unless every key of the tile is visible to
@@ -622,7 +698,7 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
-            for (int k = 0; k < 8; ++k) sv[qb][k] = s[qb][k >> 2][k & 3];
+            for (int k = 0; k < 8; ++k) sv[qb][k] = fmaf(s[qb][k >> 2][k & 3], fq[qb], cneg[qb]);
         if (!whole) {
 #pragma unroll
             for (int qb = 0; qb < QB; ++qb) {
@@ -676,6 +752,11 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
 #pragma unroll
                 for (int v = 0; v < 4; ++v)
                     pop[qb][sub * 4 + v] = (_Float16) __builtin_amdgcn_exp2f(sv[qb][sub * 4 + v]);
+            // the all-ones operand from LDS for each product (a volatile LDS
+            // read, so that it holds no registers between tiles; through a
+            // generic pointer it would become a flat load that waits for
+            // every load in flight)
+            const half8_t ones = *(const volatile __attribute__((address_space(3))) half8_t *) sOnes;
             accl[qb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pop[qb], ones, accl[qb], 0, 0, 0);
         }
         // O += P V: B operand lane l = column t*16 + n of the tile, keys
@@ -745,6 +826,7 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
     // No other workgroup reads this stripe.  (Loads of padding tiles read
     // group 0 and may see new blocks; their values are never used.)
     static_assert(!DIRECT || IPT == 1, "non-loading threads are those past the items");
+    static_assert(!DIRECT || NTHR > ITEMS, "the direct path needs threads without items to commit the chunk");
     constexpr int NL_FIRST = DIRECT ? ITEMS : 0;  // first thread without items
     uint8_t *const wring = p.base + p.g.stripe_offset(p.layer, sid, kvh);
     int i_done = 0;  // chunk keys written (wave-uniform, non-loading waves)
@@ -830,8 +912,12 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
         tile_loop(BoolC<false>{});
     // (the touched value is needed by nothing; the read must not be dropped)
     asm volatile("" ::"v"(touched));
-    // (the last barrier publishes every ring tile, so the loop has written
-    // every key; this covers nothing unless n_tiles is 0)
+    // The loop has written every key: its last barrier publishes every ring
+    // tile, after which commit_limit is n_tok, and with no ring tile at all
+    // (pos0 = 0) the limit is n_ctx >= n_tok from the first barrier on.
+    // Only a ring of fewer than 32 slots could leave keys for this call
+    // (n_ctx = 1 at a pos0 off the 32-slot grid keeps the limit at 0), and
+    // such rings take the staged path; it stays as a guard.
     if constexpr (DIRECT)
         if (!has_items) commit_until(p.n_tok);
 
@@ -896,18 +982,16 @@ constexpr int kQW = 16;
 constexpr int kQB = 1;
 constexpr int kQT = 16 * kQB * kQW;  // queries per workgroup
 
-template <int D, bool DIRECT>
-void launch_attention(const PrefillParams &p, dim3 grid, hipStream_t stream) {
-    // ring tiles 32 slots wide never wrap when n_ctx is a multiple of 32
-    if (p.g.n_ctx % kTK == 0)
-        hipLaunchKernelGGL((prefill_kernel<D, kQW, kQB, DIRECT, true>), grid, dim3(64 * kQW), 0, stream, p);
-    else
-        hipLaunchKernelGGL((prefill_kernel<D, kQW, kQB, DIRECT, false>), grid, dim3(64 * kQW), 0, stream, p);
-}
-
 template <int D>
 void launch_attention(const PrefillParams &p, bool direct, dim3 grid, hipStream_t stream) {
-    direct ? launch_attention<D, true>(p, grid, stream) : launch_attention<D, false>(p, grid, stream);
+    // ring tiles 32 slots wide never wrap when n_ctx is a multiple of 32
+    // (the direct path requires it)
+    if (direct)
+        hipLaunchKernelGGL((prefill_kernel<D, kQW, kQB, true, true>), grid, dim3(64 * kQW), 0, stream, p);
+    else if (p.g.n_ctx % kTK == 0)
+        hipLaunchKernelGGL((prefill_kernel<D, kQW, kQB, false, true>), grid, dim3(64 * kQW), 0, stream, p);
+    else
+        hipLaunchKernelGGL((prefill_kernel<D, kQW, kQB, false, false>), grid, dim3(64 * kQW), 0, stream, p);
 }
 
 }  // namespace
@@ -926,7 +1010,13 @@ static int resident_workgroups() {
     return cached[dev] > 0 ? cached[dev] : 0;
 }
 
-bool prefill_is_direct(const PrefillParams &p) { return p.n_heads == p.n_kv && p.n_tok <= kQT; }
+// The direct path: one query head per kv head, the chunk in one workgroup,
+// and ring tiles that never wrap (the per-key slots of other ring sizes do
+// not fit its register budget beside the exact block scales; those rings
+// take the staged path).
+bool prefill_is_direct(const PrefillParams &p) {
+    return p.n_heads == p.n_kv && p.n_tok <= kQT && p.g.n_ctx % kTK == 0;
+}
 
 bool launch_prefill(const PrefillParams &p, hipStream_t stream) {
     if (p.g.head_dim != 128 && p.g.head_dim != 64) return false;

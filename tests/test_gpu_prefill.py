@@ -65,7 +65,7 @@ def test_prefill_parity(gpu, pos0, n_tok):
 
 
 @pytest.mark.parametrize("n_ctx,pos0,n_tok,n_heads,n_kv", [
-    (40, 90, 30, 4, 4),     # 32-key ring tiles wrap inside the ring (one workgroup per stripe)
+    (40, 90, 30, 4, 4),     # 32-key ring tiles wrap inside the ring (staged path)
     (8, 5, 8, 4, 4),        # an 8-slot ring (the depformer's), chunk as long as the ring
     (72, 100, 60, 8, 2),    # staged chunk (4 query heads per kv head)
     (100, 1000, 100, 4, 4),
@@ -157,18 +157,19 @@ def test_prefill_argument_errors(gpu):
 
 
 def test_prefill_query_range(gpu):
-    """q enters the matrix cores as fp16 of q * scale * log2(e): a query whose
-    elements stay below 65504 after that scaling is exact to the usual bar,
-    even at 4e5; a query beyond it gets a non-finite row and leaves the other
-    queries (and the ring) unaffected."""
+    """Large query elements stay within the usual bar: each query row enters
+    the matrix cores scaled by its own power of two, so no fixed fp16 range
+    applies (4e5, 1e6 and 1e12 in three rows; a single fp16 scaling of
+    q * scale * log2(e) would overflow past about 5.1e5)."""
     n_heads, d, n_ctx, pos0, n_tok = 2, 128, 64, 100, 16
     m = Mirror(gpu, 1, 1, n_heads, d, n_ctx)
     m.fill_range(0, 0, 0, pos0, seed=77)
     q = _bf16_normals(78, (1, n_tok, n_heads, d))
     k = _bf16_normals(79, (1, n_tok, n_heads, d))
     v = _bf16_normals(80, (1, n_tok, n_heads, d))
-    q[0, 3, 0, 5] = 4.0e5   # in range: 4e5 * 0.0884 * 1.4427 = 51,000
-    q[0, 9, 1, 17] = 1.0e6  # out of range (127,500 > 65504)
+    q[0, 3, 0, 5] = 4.0e5
+    q[0, 9, 1, 17] = 1.0e6
+    q[0, 12, 0, 100] = 1.0e12
     q = oracle.round_bf16(q)
     out = gpu.full((1, n_tok, n_heads, d), float("nan"), dtype=gpu.float32, device="cuda")
     m.ring.prefill(0, _i32(gpu, [pos0]), m.dev(q, gpu.bfloat16), m.dev(k, gpu.bfloat16),
@@ -177,10 +178,5 @@ def test_prefill_query_range(gpu):
     got = out.cpu().numpy()[0]
     kc, vc = m.orc[(0, 0)]
     ref = oracle.ring_prefill_f64(kc, vc, pos0, q[0], k[0], v[0], n_heads)
-    bad = np.zeros((n_tok, n_heads), bool)
-    bad[9, 1] = True
-    assert not np.all(np.isfinite(got[9, 1])), "out-of-range query must not pass silently"
-    check_close(got[~bad], ref[~bad], "queries in range")
-    for i in range(n_tok):
-        m.oracle_append(0, 0, pos0 + i, k[0, i], v[0, i])
-    m.assert_ring_equal(0, 0)
+    check_close(got, ref, "large query elements")
+    m.assert_ring_equal(0, 0)   # (the oracle's prefill appended the chunk)
