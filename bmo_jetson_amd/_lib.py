@@ -52,6 +52,13 @@ SIGNATURES = {
     "bmo_attn_session_has_graph": (i32, [P]),
     "bmo_attn_session_replay": (i32, [P, i32]),
     "bmo_attn_session_last_error": (ctypes.c_char_p, [P]),
+    "bmo_attn_session_begin_step": (i32, [P, i32]),
+    "bmo_attn_session_layer": (i32, [P, i32, P, P, P, P]),
+    "bmo_attn_session_end_step": (i32, [P]),
+    "bmo_attn_session_reset_async": (i32, [P]),
+    "bmo_attn_session_sync": (i32, [P]),
+    "bmo_attn_session_capture_begin": (i32, [P]),
+    "bmo_attn_session_capture_end": (i32, [P]),
 }
 
 

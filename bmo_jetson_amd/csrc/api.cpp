@@ -63,7 +63,10 @@ void warn_once(std::atomic<bool> &warned, const char *fn, const char *why) {
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+thread_local std::string t_last_fail;  // the calling thread's last ring failure
+
 int fail(bmo_kv_ring_t *r, int code, const std::string &msg) {
+    t_last_fail = msg;
     if (r) {
         std::lock_guard<std::mutex> lk(r->mu);
         r->last_error = msg;
@@ -165,6 +168,8 @@ void write_block(const bmo::RingGeom &g, std::vector<uint8_t> &buf, int first, i
 }
 
 }  // namespace
+
+const char *bmo::ring_thread_last_error() { return t_last_fail.c_str(); }
 
 extern "C" {
 

@@ -116,6 +116,9 @@ bool launch_gemv(const GemvParams &p, hipStream_t stream);
 // True when launch_prefill runs one attention kernel that quantizes and
 // commits the chunk itself (no staging stripes are read or written).
 bool prefill_is_direct(const PrefillParams &p);
+// Message of the last ring call that failed on the calling thread (empty if
+// none): unlike the ring's own message, no other thread's call can replace it.
+const char *ring_thread_last_error();
 // Writes the zero state (ring_layout.hpp) into n_ranges ranges of
 // range_bytes bytes (a multiple of the group size) spaced range_stride apart.
 void launch_clear(uint8_t *base, int64_t range_bytes, int64_t range_stride, int n_ranges,

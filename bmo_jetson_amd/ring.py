@@ -22,6 +22,7 @@ class RingError(RuntimeError):
     def __init__(self, fn: str, rc: int, msg: str | None):
         super().__init__(f"{fn} rc={rc}: {msg or 'unknown'}")
         self.rc = rc
+        self.msg = msg or ""
 
 
 def _ptr(x) -> int | None:
@@ -233,7 +234,14 @@ class Session:
     append + attention through every layer at a position and advances it,
     ``capture`` / ``replay`` do the same from a HIP graph recorded in the
     library.  q/out are [n_layers][n_heads][head_dim] and k/v
-    [n_layers][n_kv_heads][head_dim] fp32 device buffers."""
+    [n_layers][n_kv_heads][head_dim] fp32 device buffers.
+
+    At a model's layer granularity, ``begin_step(pos)``, ``layer(l, q, k, v,
+    out)`` per layer and ``end_step()`` queue the step one layer at a time on
+    ``stream``, where the caller's own kernels (projections, FFN) fall
+    between them; ``capture_begin()`` / ``capture_end()`` record whatever is
+    queued on the stream in between (a frame may start with
+    ``reset_async()``), and ``replay`` runs it."""
 
     def __init__(self, ring: KVRing, session: int, n_heads: int, scale: float = 0.0,
                  rope_theta: float = 0.0):
@@ -302,8 +310,30 @@ class Session:
     def has_graph(self) -> bool:
         return bool(lib().bmo_attn_session_has_graph(self._h))
 
-    def replay(self, pos: int) -> None:
+    def replay(self, pos: int = 0) -> None:
         self._check("bmo_attn_session_replay", lib().bmo_attn_session_replay(self._h, int(pos)))
+
+    def begin_step(self, pos: int) -> None:
+        self._check("bmo_attn_session_begin_step", lib().bmo_attn_session_begin_step(self._h, int(pos)))
+
+    def layer(self, layer: int, q, k, v, out) -> None:
+        self._check("bmo_attn_session_layer", lib().bmo_attn_session_layer(
+            self._h, int(layer), _ptr(q), _ptr(k), _ptr(v), _ptr(out)))
+
+    def end_step(self) -> None:
+        self._check("bmo_attn_session_end_step", lib().bmo_attn_session_end_step(self._h))
+
+    def reset_async(self) -> None:
+        self._check("bmo_attn_session_reset_async", lib().bmo_attn_session_reset_async(self._h))
+
+    def sync(self) -> None:
+        self._check("bmo_attn_session_sync", lib().bmo_attn_session_sync(self._h))
+
+    def capture_begin(self) -> None:
+        self._check("bmo_attn_session_capture_begin", lib().bmo_attn_session_capture_begin(self._h))
+
+    def capture_end(self) -> None:
+        self._check("bmo_attn_session_capture_end", lib().bmo_attn_session_capture_end(self._h))
 
 
 def launch_decode_attention(q, k, v, k_cache, v_cache, out, head_dim: int, n_heads: int,

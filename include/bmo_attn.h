@@ -316,7 +316,8 @@ BMO_ATTN_API void bmo_attn_session_free(bmo_attn_session_t *s);
  * K/V part of bmo_reset, src/bmo_api.cpp:258-272). */
 BMO_ATTN_API int bmo_attn_session_reset(bmo_attn_session_t *s);
 
-/* The next position (the one after the last completed step); -1 for NULL. */
+/* The position the next step uses once the queued work has run (the one
+ * after the last step run or queued); -1 for NULL. */
 BMO_ATTN_API int64_t bmo_attn_session_pos(bmo_attn_session_t *s);
 
 /* The handle's HIP stream (hipStream_t as void*). */
@@ -329,10 +330,11 @@ BMO_ATTN_API void *bmo_attn_session_stream(bmo_attn_session_t *s);
 BMO_ATTN_API int bmo_attn_session_forward(bmo_attn_session_t *s, int pos, const float *q,
                                           const float *k, const float *v, float *out);
 
-/* Records one token step over these buffers into a HIP graph (replacing a
- * previous one); the graph reads the position from device memory and ends
- * by advancing it.  Nothing runs and the position does not change.  The
- * buffers must stay valid while the graph is kept.  Stands in for
+/* Records one token step over these buffers into a HIP graph; the graph
+ * reads the position from device memory and ends by advancing it.  Nothing
+ * runs and the position does not change.  The buffers must stay valid while
+ * the graph is kept.  A previous graph is replaced only once the new one is
+ * instantiated (a failed capture keeps it).  Stands in for
  * bmo_capture_graphs (src/bmo_api.cpp:334-351). */
 BMO_ATTN_API int bmo_attn_session_capture(bmo_attn_session_t *s, const float *q, const float *k,
                                           const float *v, float *out);
@@ -341,12 +343,70 @@ BMO_ATTN_API int bmo_attn_session_capture(bmo_attn_session_t *s, const float *q,
  * src/bmo_api.cpp:353-359). */
 BMO_ATTN_API int bmo_attn_session_has_graph(bmo_attn_session_t *s);
 
-/* Replays the captured step at position pos (same range as forward) on the
- * handle's stream and returns when it is done; the captured buffers hold the
- * step's q/k/v on entry and its output on return.  Afterwards the position
- * is pos + 1.  Replaying at the handle's current position costs one graph
- * launch; another position first sets the device position. */
+/* Replays the captured graph (bmo_attn_session_capture, or _capture_begin /
+ * _end) on the handle's stream and returns when it is done; the captured
+ * buffers hold the inputs on entry and the outputs on return.  A graph that
+ * does not begin with a reset runs at position pos (same range as forward;
+ * replaying at the handle's current position costs one graph launch, another
+ * position first sets the device position) and leaves the position at pos +
+ * its steps; a graph that begins with bmo_attn_session_reset_async ignores
+ * pos and leaves the position at its steps. */
 BMO_ATTN_API int bmo_attn_session_replay(bmo_attn_session_t *s, int pos);
+
+/* ---- the handle at a model's layer granularity ----
+ * The reference's layer loop (src/bmo_compute.cpp:2188-2641, driven by
+ * bmo_forward_temporal2, src/bmo_api.cpp:384-511) computes layer l+1's q/k/v
+ * from layer l's attention output: the output projection (:2423), the FFN
+ * and the next QKV projection (:2232) run between two attention calls.  These
+ * calls queue one layer at a time on the handle's stream
+ * (bmo_attn_session_stream), so the caller's own kernels on that stream fall
+ * between them in stream order; none of them waits for the GPU.  A step is
+ *   begin_step(pos), then layer(l, ...) for the layers in any order, then
+ *   end_step();
+ * every layer call of a step reads the same device position.  Between
+ * capture_begin and capture_end the calls (and the caller's kernels on the
+ * handle's stream) are recorded instead of run; replay then runs them. */
+
+/* Sets the position the next layer calls use to pos (0 <= pos <= 2^31 - 2),
+ * queued on the stream (nothing is queued when it already holds pos).  Not
+ * allowed during a capture: a captured step takes its position from replay. */
+BMO_ATTN_API int bmo_attn_session_begin_step(bmo_attn_session_t *s, int pos);
+
+/* Queues layer `layer`'s fused append + attention at the current device
+ * position (with RoPE when the handle has rope_theta > 0): the arguments of
+ * one layer of bmo_attn_session_forward, q/out [n_heads][head_dim] and k/v
+ * [n_kv_heads][head_dim] fp32 device buffers, read and written when the
+ * stream reaches the call (the attention node of src/bmo_compute.cpp:2293-2418,
+ * and of the depth loop, :2945-2991). */
+BMO_ATTN_API int bmo_attn_session_layer(bmo_attn_session_t *s, int layer, const float *q,
+                                        const float *k, const float *v, float *out);
+
+/* Queues the advance of the device position by one that ends a step
+ * (h->pos = pos + 1, src/bmo_api.cpp:501); bmo_attn_session_pos reports the
+ * advanced position at once. */
+BMO_ATTN_API int bmo_attn_session_end_step(bmo_attn_session_t *s);
+
+/* Queues the zeroing of the session's K/V in every layer and position 0:
+ * bmo_attn_session_reset without the wait, so that a capture can begin with
+ * it (the depformer's per-frame reset in bmo_forward_depth_cascade,
+ * src/bmo_api.cpp:668-743 with the reset at :682). */
+BMO_ATTN_API int bmo_attn_session_reset_async(bmo_attn_session_t *s);
+
+/* Waits for everything queued on the handle's stream; reports a HIP error
+ * the queued work raised. */
+BMO_ATTN_API int bmo_attn_session_sync(bmo_attn_session_t *s);
+
+/* Starts recording the handle's stream into a HIP graph (thread-local
+ * capture mode: the caller's other HIP calls on this thread must not
+ * allocate or synchronize until capture_end).  forward, capture, replay,
+ * reset, begin_step and sync are rejected until capture_end. */
+BMO_ATTN_API int bmo_attn_session_capture_begin(bmo_attn_session_t *s);
+
+/* Ends the recording and keeps it as the handle's graph (replacing a previous
+ * one only once the new one is instantiated).  If a handle call inside the
+ * capture failed, the recording is discarded, the previous graph kept and an
+ * error returned.  The position does not change. */
+BMO_ATTN_API int bmo_attn_session_capture_end(bmo_attn_session_t *s);
 
 /* Message of the handle's most recent failed call, or (s == NULL) of the
  * calling thread's last failed create; NULL if none.  Owned by the library
