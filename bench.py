@@ -3,21 +3,25 @@
 
 Default workload: one step = decode attention of 64
 sessions through 32 layers (32 launches), 32 heads x head_dim 128, full
-W=512 windows at per-session positions drawn from U[512, 4096), K/V from
-N(0,1) with each element scaled x8 with probability 1%, quantized to Q4_0 by
-the library's own append kernel.  The ring (4.83 GB) is resident in HBM
-before timing starts.
+W=512 windows at per-session positions in [512, 4096), K/V ~N(0,1) with each
+element scaled x8 with probability 1%, quantized to Q4_0 by the library's
+own write kernel.  The ring (4.83 GB) is resident in HBM before timing
+starts.  Every input is the configuration's seeded stream (splitmix64 +
+Box-Muller, seeds 0xB0A00001..5; layouts in fill_ring, run_decode and each
+leg), generated on the GPU by libbmo_synth.so, bit for bit the stream the
+CPU restates, so any part of it can be regenerated from the seed.
 
 value = algorithmic bytes per step / step time, where the algorithmic bytes
 of one (session, layer) are the full window's Q4_0 K+V bytes
 (W*H*2*(D/32)*18) plus q and out in fp32 (2*H*D*4): 2,392,064 B, so
 4,898,947,072 B per step.
 
-The step (32 launches, one per layer) is captured in a HIP graph and
-replayed; the timed region is exactly --steps replays between two
-synchronizations, timed by a HIP event pair on the replay stream.  The
-roofline entry divides one launch's algorithmic bytes by the mean launch
-duration from that region (step time / 32, kernel gaps included).
+The step (32 launches, one per layer) is captured in a HIP graph before the
+ring is filled; after the fill, one eager step, --warmup untimed replays and
+exactly --steps timed replays between two synchronizations, timed by a HIP
+event pair on the replay stream.  The roofline entry divides one launch's
+algorithmic bytes by the mean launch duration from that region (step time /
+32, kernel gaps included).
 
 Also reported: BASELINE config 4 (256 sessions, fused append + decode, timed
 the same way, with its own roofline entry), B=1 latency (one layer, 32 heads, W=512,
@@ -70,22 +74,36 @@ def read_traffic(config):
     return None
 
 
-def fill_ring(torch, ring, L, S, H, D, W, pos_host, seed, outlier_p=0.01):
-    gen = torch.Generator(device="cuda")
-    gen.manual_seed(seed)
+def fill_ring(torch, ring, L, S, H, D, W, pos_end, seed, outliers=True):
+    """Writes each session's window of positions pos_end[s] - W + 1 ..
+    pos_end[s] in every layer.  K of (layer l, session s, window slot j
+    (position pos_end[s] - W + 1 + j), head h, dim d) is element
+    (((l S + s) W + j) H + h) D + d of the seeded stream `seed` (x8 with
+    probability 1% when `outliers`), V the same element of stream seed + 1;
+    generated on the GPU by libbmo_synth.so, bit for bit the CPU's
+    restatement."""
+    from bmo_jetson_amd.synth import fill_normal
+
     stream = torch.cuda.current_stream()
+    k = torch.empty((S, W, H, D), device="cuda")
+    v = torch.empty((S, W, H, D), device="cuda")
     for layer in range(L):
-        k = torch.randn((S, W, H, D), device="cuda", generator=gen)
-        v = torch.randn((S, W, H, D), device="cuda", generator=gen)
-        if outlier_p > 0:
-            k.mul_(torch.where(torch.rand((S, W, H, D), device="cuda", generator=gen) < outlier_p,
-                               8.0, 1.0))
-            v.mul_(torch.where(torch.rand((S, W, H, D), device="cuda", generator=gen) < outlier_p,
-                               8.0, 1.0))
+        off = layer * S * W * H * D
+        fill_normal(k, seed, off, outliers, stream=stream)
+        fill_normal(v, seed + 1, off, outliers, stream=stream)
         for s in range(S):
-            ring.write(layer, s, int(pos_host[s]) - W + 1, k[s], v[s], stream=stream)
-        del k, v
+            ring.write(layer, s, int(pos_end[s]) - W + 1, k[s], v[s], stream=stream)
     torch.cuda.synchronize()
+    del k, v
+
+
+def synth(torch, shape, seed, offset=0):
+    """A device tensor of `shape` holding elements offset.. of stream seed."""
+    from bmo_jetson_amd.synth import fill_normal
+
+    t = torch.empty(shape, device="cuda")
+    fill_normal(t, seed, offset, stream=torch.cuda.current_stream())
+    return t
 
 
 def capture_graph(torch, launch):
@@ -101,29 +119,29 @@ def capture_graph(torch, launch):
     return graph
 
 
-def time_steps(torch, launch_layer, n_layers, steps, warmup):
-    """Runs one eager step, captures one step (n_layers launches, one per
-    layer, as the model runs them) into a HIP graph, replays it `warmup` times
-    (the untimed warmup steps, right before the timed region, so that the GPU
-    enters it at its working clocks: after the idle spell of the graph capture
-    the first milliseconds of work ran about 2% slower), and times exactly
-    `steps` replays between two torch.cuda.synchronize() calls with a HIP
-    event pair recorded on the replay stream.  Returns ms per step; the mean
-    launch duration is that over n_layers (it includes the small gaps between
-    the graph's kernels, so it is an upper bound on the kernel time).  Then
-    `steps` more replays, each between its own event pair, give the per-step
-    distribution (median, min, max), outside the timed region."""
-    stream = torch.cuda.current_stream()
-    for layer in range(n_layers):
-        launch_layer(layer, stream)
-    torch.cuda.synchronize()
-
+def time_steps(torch, launch_layer, n_layers, steps, warmup, prepare=None):
+    """Captures one step (n_layers launches, one per layer, as the model runs
+    them) into a HIP graph, then runs prepare() (the inputs' generation and
+    the ring fill: capture needs only the buffers' addresses, so the GPU's
+    heavy setup work ends right before the timed part instead of an idle
+    spell of capturing, after which the first milliseconds of work ran about
+    2% slower), one eager step, `warmup` untimed graph replays, and exactly
+    `steps` replays between two torch.cuda.synchronize() calls, timed with a
+    HIP event pair recorded on the replay stream.  Returns ms per step; the
+    mean launch duration is that over n_layers (it includes the small gaps
+    between the graph's kernels, so it is an upper bound on the kernel time).
+    Then `steps` more replays, each between its own event pair, give the
+    per-step distribution (median, min, max), outside the timed region."""
     def whole_step(st):
         for layer in range(n_layers):
             launch_layer(layer, st)
 
     graph = capture_graph(torch, whole_step)
-    for _ in range(max(1, warmup)):
+    if prepare is not None:
+        prepare()
+    stream = torch.cuda.current_stream()
+    whole_step(stream)
+    for _ in range(warmup):
         graph.replay()
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
@@ -178,17 +196,14 @@ def bench_b1(torch, iters=200):
     from an eager loop (Python launch cost included)."""
     from bmo_jetson_amd import KVRing
 
-    H, D, W, P = 32, 128, 512, 700
+    H, D, W, P, seed = 32, 128, 512, 700, 0xB0A00001
     ring = KVRing(1, 1, H, D, W)
-    pos_host = np.array([P], np.int64)
-    fill_ring(torch, ring, 1, 1, H, D, W, pos_host, 0xB0A00001, outlier_p=0.0)
+    # the ring holds positions 189..700 (streams seed, seed + 1); q, k, v are
+    # streams seed + 2, + 3, + 4 (the fused call appends k, v at 700 again)
+    fill_ring(torch, ring, 1, 1, H, D, W, [P], seed, outliers=False)
     stream = torch.cuda.current_stream()
     pos = torch.tensor([P], dtype=torch.int32, device="cuda")
-    g = torch.Generator(device="cuda")
-    g.manual_seed(0xB0A00001)
-    q = torch.randn(H * D, device="cuda", generator=g)
-    k = torch.randn(H * D, device="cuda", generator=g)
-    v = torch.randn(H * D, device="cuda", generator=g)
+    q, k, v = (synth(torch, (H * D,), seed + i) for i in (2, 3, 4))
     out = torch.empty(H * D, device="cuda")
     res = {}
     calls = {
@@ -249,14 +264,10 @@ def bench_b1_cold(torch, replicas=8):
     Microseconds per launch from HIP-graph replays of `replicas` steps."""
     from bmo_jetson_amd import KVRing
 
-    H, D, W, P, L = 32, 128, 512, 700, 32
+    H, D, W, P, L, seed = 32, 128, 512, 700, 32, 0xB0A00011
     ring = KVRing(L, replicas, H, D, W)
-    fill_ring(torch, ring, L, replicas, H, D, W, np.full(replicas, P), 0xB0A00011, outlier_p=0.0)
-    g = torch.Generator(device="cuda")
-    g.manual_seed(0xB0A00011)
-    q = torch.randn((L, H * D), device="cuda", generator=g)
-    k = torch.randn((L, H * D), device="cuda", generator=g)
-    v = torch.randn((L, H * D), device="cuda", generator=g)
+    fill_ring(torch, ring, L, replicas, H, D, W, [P] * replicas, seed, outliers=False)
+    q, k, v = (synth(torch, (L, H * D), seed + i) for i in (2, 3, 4))
     out = torch.empty((L, H * D), device="cuda")
     pos = torch.tensor([P], dtype=torch.int32, device="cuda")
     sids = [torch.tensor([r], dtype=torch.int32, device="cuda") for r in range(replicas)]
@@ -287,13 +298,10 @@ def bench_depformer(torch, frames=20):
     8-slot ring, step s attends to steps 0..s), replayed from a HIP graph."""
     from bmo_jetson_amd import KVRing
 
-    L, H, D, W, STEPS = 6, 16, 64, 8, 8
+    L, H, D, W, STEPS, seed = 6, 16, 64, 8, 8, 0xB0A00002
     ring = KVRing(L, 1, H, D, W)
-    g = torch.Generator(device="cuda")
-    g.manual_seed(0xB0A00002)
-    q = torch.randn((STEPS, L, H * D), device="cuda", generator=g)
-    k = torch.randn((STEPS, L, H * D), device="cuda", generator=g)
-    v = torch.randn((STEPS, L, H * D), device="cuda", generator=g)
+    # q, k, v of (step, layer, head, dim): streams seed, seed + 1, seed + 2
+    q, k, v = (synth(torch, (STEPS, L, H * D), seed + i) for i in (0, 1, 2))
     out = torch.empty((STEPS, L, H * D), device="cuda")
     pos = [torch.tensor([s], dtype=torch.int32, device="cuda") for s in range(STEPS)]
 
@@ -332,18 +340,16 @@ def bench_prefill(torch, reps=10):
     and empty (p0 = 0).  Timed as HIP-graph replays."""
     from bmo_jetson_amd import KVRing
 
-    S, C, W, H, D = 16, 256, 512, 32, 128
+    S, C, W, H, D, seed = 16, 256, 512, 32, 128, 0xB0A00005
     res = {"workload": "cfg5: S=16 sessions x C=256 tokens, W=512, H=32, D=128, bf16 q/k/v, "
                        "causal + window mask; one layer per call"}
     for name, p0 in (("full", 1024), ("empty", 0)):
         ring = KVRing(1, S, H, D, W)
-        if p0:
-            fill_ring(torch, ring, 1, S, H, D, W, np.full(S, p0 - 1), 0xB0A00005, outlier_p=0.0)
-        g = torch.Generator(device="cuda")
-        g.manual_seed(0xB0A00005 + p0)
-        q = torch.randn((S, C, H, D), device="cuda", generator=g).to(torch.bfloat16)
-        k = torch.randn((S, C, H, D), device="cuda", generator=g).to(torch.bfloat16)
-        v = torch.randn((S, C, H, D), device="cuda", generator=g).to(torch.bfloat16)
+        if p0:  # history: positions p0 - W .. p0 - 1 (streams seed, seed + 1)
+            fill_ring(torch, ring, 1, S, H, D, W, [p0 - 1] * S, seed, outliers=False)
+        # the chunk's q, k, v (session, token, head, dim): streams seed + 2,
+        # + 3, + 4 rounded to bf16 (nearest even)
+        q, k, v = (synth(torch, (S, C, H, D), seed + i).to(torch.bfloat16) for i in (2, 3, 4))
         out = torch.empty((S, C, H, D), device="cuda")
         pos0 = torch.full((S,), p0, dtype=torch.int32, device="cuda")
         call = lambda st: ring.prefill(0, pos0, q, k, v, out, H, n_tok=C, stream=st)
@@ -420,24 +426,33 @@ def run_decode(torch, config, steps, warmup, sessions=None):
     H, D, W, L = 32, 128, 512, 32
     S = sessions or (64 if config == "cfg3" else 256)
     fused = config == "cfg4"
-    seed = 0xB0A00003 if config == "cfg3" else 0xB0A00004
-    rng = np.random.default_rng(seed)
-    pos_host = rng.integers(512, 4096, size=S).astype(np.int64)
-    log(f"[bench] {config}: S={S} L={L} H={H} D={D} W={W} fused={fused}; filling ring")
-    t_fill = time.time()
-    ring = KVRing(L, S, H, D, W)
-    # cfg4 appends the token at pos, so the ring holds the window before it
-    fill_ring(torch, ring, L, S, H, D, W, pos_host - (1 if fused else 0), seed)
-    log(f"[bench] ring {ring.nbytes / 1e9:.2f} GB filled in {time.time() - t_fill:.1f} s")
+    from bmo_jetson_amd.synth import positions
 
+    seed = 0xB0A00003 if config == "cfg3" else 0xB0A00004
+    pos_host = np.array(positions(seed, S), dtype=np.int64)
+    ring = KVRing(L, S, H, D, W)
     pos = torch.tensor(pos_host, dtype=torch.int32, device="cuda")
-    g = torch.Generator(device="cuda")
-    g.manual_seed(seed + 7)
-    q = torch.randn((L, S, H, D), device="cuda", generator=g)
+    q = torch.empty((L, S, H, D), device="cuda")
     out = torch.empty((L, S, H, D), device="cuda")
     if fused:
-        kn = torch.randn((L, S, H, D), device="cuda", generator=g)
-        vn = torch.randn((L, S, H, D), device="cuda", generator=g)
+        kn = torch.empty((L, S, H, D), device="cuda")
+        vn = torch.empty((L, S, H, D), device="cuda")
+
+    def prepare():
+        log(f"[bench] {config}: S={S} L={L} H={H} D={D} W={W} fused={fused}; filling ring")
+        t_fill = time.time()
+        # cfg4 appends the token at pos, so the ring holds the window before it
+        fill_ring(torch, ring, L, S, H, D, W, pos_host - (1 if fused else 0), seed)
+        # q (layer, session, head, dim): stream seed + 2; cfg4's new K/V rows:
+        # streams seed + 3, seed + 4
+        from bmo_jetson_amd.synth import fill_normal
+        st = torch.cuda.current_stream()
+        fill_normal(q, seed + 2, stream=st)
+        if fused:
+            fill_normal(kn, seed + 3, stream=st)
+            fill_normal(vn, seed + 4, stream=st)
+        torch.cuda.synchronize()
+        log(f"[bench] ring {ring.nbytes / 1e9:.2f} GB filled in {time.time() - t_fill:.1f} s")
 
     def launch_layer(layer, st):
         if fused:
@@ -445,7 +460,7 @@ def run_decode(torch, config, steps, warmup, sessions=None):
         else:
             ring.decode(layer, pos, q[layer], out[layer], H, stream=st)
 
-    ms_per_step, per_step = time_steps(torch, launch_layer, L, steps, warmup)
+    ms_per_step, per_step = time_steps(torch, launch_layer, L, steps, warmup, prepare)
     launch_ms = ms_per_step / L
     per_step_bytes = unit_bytes(H, D, W) * S * L
     if fused:

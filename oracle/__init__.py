@@ -61,6 +61,9 @@ def lib() -> ctypes.CDLL:
             "orc_rope_interleaved": (None, [P, P, i32, i32, i64, f64]),
             "orc_mix64": (u64, [u64]),
             "orc_fill_normal": (None, [u64, u64, P, i64]),
+            "orc_fill_kv": (None, [u64, u64, P, i64]),
+            "orc_synth_ln": (f64, [f64]),
+            "orc_synth_cos2pi": (f64, [f64]),
             "orc_fill_u64": (None, [u64, u64, P, i64]),
             "orc_round_bf16": (ctypes.c_float, [ctypes.c_float]),
             "orc_cpu_decode_f32": (None, [P, P, i32, i32, i32, i32, i64, P, P, P]),
@@ -226,6 +229,13 @@ def rope_interleaved(x: np.ndarray, pos: int, theta: float = 10000.0) -> np.ndar
 def normal(seed: int, n: int, offset: int = 0) -> np.ndarray:
     out = np.empty(n, dtype=np.float32)
     lib().orc_fill_normal(seed & (2**64 - 1), offset, _p(out), n)
+    return out
+
+
+def kv_normal(seed: int, n: int, offset: int = 0) -> np.ndarray:
+    """normal(), each element x8 with probability 1% (configurations 3, 4)."""
+    out = np.empty(n, dtype=np.float32)
+    lib().orc_fill_kv(seed & (2**64 - 1), offset, _p(out), n)
     return out
 
 

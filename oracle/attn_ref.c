@@ -189,15 +189,111 @@ void orc_fill_u64(uint64_t seed, uint64_t offset, uint64_t *out, int64_t n) {
     }
 }
 
-/* Box-Muller on two splitmix64 words per element (cosine branch only). */
+/* The synthetic input stream of the benchmark configurations (the seeds and
+ * layouts are listed with the configurations): element c of stream `seed` is
+ * a Box-Muller normal of two splitmix64 words, cosine branch only,
+ *   a = mix64(seed ^ mix64(2c)),  b = mix64(seed ^ mix64(2c + 1)),
+ *   u1 = (a >> 11) + 0.5) 2^-53,  u2 = (b >> 11) 2^-53,
+ *   z = (float) (sqrt(-2 ln u1) cos(2 pi u2)),
+ * with ln and cos(2 pi .) evaluated from +, -, *, / and sqrt alone (no fused
+ * multiply-add, no library transcendental), each correctly rounded in
+ * IEEE double, so that a device implementation of the same steps gives the
+ * same bits.  The "kv" variant multiplies an element by 8 when a third word,
+ * mix64((seed ^ 0xD1B54A32D192ED03) ^ mix64(c)), has its top 32 bits below
+ * 42949673 (probability 0.0100000000093). */
+
+/* ln x for x in [2^-54, 1]: x = m 2^e with m in [sqrt(1/2), sqrt(2)], ln x =
+ * e ln 2 + 2 atanh(s), s = (m - 1)/(m + 1), |s| <= 0.1716, the atanh series
+ * to s^21 (the next term is below 2^-55 of the sum). */
+static double synth_ln(double x) {
+    uint64_t bits;
+    memcpy(&bits, &x, sizeof bits);
+    int e = (int) ((bits >> 52) & 0x7FF) - 1023;
+    bits = (bits & 0x000FFFFFFFFFFFFFull) | 0x3FF0000000000000ull;
+    double m;
+    memcpy(&m, &bits, sizeof m);
+    if (m > 0x1.6a09e667f3bcdp+0) {  /* sqrt(2) */
+        m = m * 0.5;
+        e = e + 1;
+    }
+    const double s = (m - 1.0) / (m + 1.0);
+    const double s2 = s * s;
+    double p = 0x1.8618618618618p-5;            /* 1/21 */
+    p = p * s2 + 0x1.af286bca1af28p-5;          /* 1/19 */
+    p = p * s2 + 0x1.e1e1e1e1e1e1ep-5;          /* 1/17 */
+    p = p * s2 + 0x1.1111111111111p-4;          /* 1/15 */
+    p = p * s2 + 0x1.3b13b13b13b14p-4;          /* 1/13 */
+    p = p * s2 + 0x1.745d1745d1746p-4;          /* 1/11 */
+    p = p * s2 + 0x1.c71c71c71c71cp-4;          /* 1/9 */
+    p = p * s2 + 0x1.2492492492492p-3;          /* 1/7 */
+    p = p * s2 + 0x1.999999999999ap-3;          /* 1/5 */
+    p = p * s2 + 0x1.5555555555555p-2;          /* 1/3 */
+    p = p * s2 + 1.0;
+    return (double) e * 0x1.62e42fefa39efp-1 + 2.0 * (s * p);   /* ln 2 */
+}
+
+/* cos(2 pi t) for t in [0, 1): quadrant n = floor(4t), g = 4t - n (both
+ * exact), cos(pi/2 (n + g)) = cos y, -sin y, -cos y, sin y for n = 0..3 with
+ * y = pi/2 g; g > 1/2 is folded to 1 - g with cos and sin swapped, so
+ * y <= pi/4 and the Taylor series to y^16 (cos) or y^17 (sin) suffice. */
+static double synth_cos2pi(double t) {
+    const double t4 = t * 4.0;
+    const int n = (int) t4;
+    double g = t4 - (double) n;
+    int use_sin = n & 1;
+    const int neg = n == 1 || n == 2;
+    if (g > 0.5) {
+        g = 1.0 - g;
+        use_sin ^= 1;
+    }
+    const double y = g * 0x1.921fb54442d18p+0;  /* pi/2 */
+    const double y2 = y * y;
+    double r;
+    if (use_sin) {
+        double p = 0x1.952c77030ad4ap-49;       /* 1/17! */
+        p = 0x1.ae7f3e733b81fp-41 - y2 * p;     /* 1/15! */
+        p = 0x1.6124613a86d09p-33 - y2 * p;     /* 1/13! */
+        p = 0x1.ae64567f544e4p-26 - y2 * p;     /* 1/11! */
+        p = 0x1.71de3a556c734p-19 - y2 * p;     /* 1/9! */
+        p = 0x1.a01a01a01a01ap-13 - y2 * p;     /* 1/7! */
+        p = 0x1.1111111111111p-7 - y2 * p;      /* 1/5! */
+        p = 0x1.5555555555555p-3 - y2 * p;      /* 1/3! */
+        p = 1.0 - y2 * p;
+        r = y * p;
+    } else {
+        double p = 0x1.ae7f3e733b81fp-45;       /* 1/16! */
+        p = 0x1.93974a8c07c9dp-37 - y2 * p;     /* 1/14! */
+        p = 0x1.1eed8eff8d898p-29 - y2 * p;     /* 1/12! */
+        p = 0x1.27e4fb7789f5cp-22 - y2 * p;     /* 1/10! */
+        p = 0x1.a01a01a01a01ap-16 - y2 * p;     /* 1/8! */
+        p = 0x1.6c16c16c16c17p-10 - y2 * p;     /* 1/6! */
+        p = 0x1.5555555555555p-5 - y2 * p;      /* 1/4! */
+        p = 0.5 - y2 * p;                       /* 1/2! */
+        r = 1.0 - y2 * p;
+    }
+    return neg ? -r : r;
+}
+
+static float synth_normal(uint64_t seed, uint64_t c) {
+    const uint64_t a = orc_mix64(seed ^ orc_mix64(2 * c));
+    const uint64_t b = orc_mix64(seed ^ orc_mix64(2 * c + 1));
+    const double u1 = ((double) (a >> 11) + 0.5) * 0x1p-53;
+    const double u2 = (double) (b >> 11) * 0x1p-53;
+    return (float) (sqrt(-2.0 * synth_ln(u1)) * synth_cos2pi(u2));
+}
+
 void orc_fill_normal(uint64_t seed, uint64_t offset, float *out, int64_t n) {
-    const double two_pi = 6.283185307179586476925286766559;
+    for (int64_t i = 0; i < n; ++i) out[i] = synth_normal(seed, offset + (uint64_t) i);
+}
+
+void orc_fill_kv(uint64_t seed, uint64_t offset, float *out, int64_t n) {
     for (int64_t i = 0; i < n; ++i) {
         const uint64_t c = offset + (uint64_t) i;
-        const uint64_t a = orc_mix64(seed ^ orc_mix64(2 * c));
-        const uint64_t b = orc_mix64(seed ^ orc_mix64(2 * c + 1));
-        const double u1 = ((double) (a >> 11) + 0.5) * (1.0 / 9007199254740992.0);
-        const double u2 = (double) (b >> 11) * (1.0 / 9007199254740992.0);
-        out[i] = (float) (sqrt(-2.0 * log(u1)) * cos(two_pi * u2));
+        const float z = synth_normal(seed, c);
+        const uint64_t w = orc_mix64((seed ^ 0xD1B54A32D192ED03ull) ^ orc_mix64(c));
+        out[i] = (w >> 32) < 42949673u ? z * 8.0f : z;
     }
 }
+
+double orc_synth_ln(double x) { return synth_ln(x); }
+double orc_synth_cos2pi(double t) { return synth_cos2pi(t); }

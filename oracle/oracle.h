@@ -161,8 +161,15 @@ void orc_ring_copy_k_f32(const orc_block_q4_0 *kc, int n_heads, int head_dim,
 
 /* ---- seeded synthetic inputs ----------------------------------------------- */
 uint64_t orc_mix64(uint64_t x);
-/* n standard normals, element i a pure function of (seed, offset + i). */
+/* n standard normals, element i a pure function of (seed, offset + i): the
+ * synthetic input stream of the benchmark configurations (attn_ref.c). */
 void orc_fill_normal(uint64_t seed, uint64_t offset, float *out, int64_t n);
+/* The same normals, each multiplied by 8 with probability 1% (a third word
+ * per element decides): the K/V of configurations 3 and 4. */
+void orc_fill_kv(uint64_t seed, uint64_t offset, float *out, int64_t n);
+/* The stream's ln (x in [2^-54, 1]) and cos(2 pi t) (t in [0, 1)). */
+double orc_synth_ln(double x);
+double orc_synth_cos2pi(double t);
 /* uniform 64-bit words, element i a pure function of (seed, offset + i). */
 void orc_fill_u64(uint64_t seed, uint64_t offset, uint64_t *out, int64_t n);
 /* fp32 -> bf16 -> fp32, round to nearest even (NaN kept quiet). */

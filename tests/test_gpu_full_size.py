@@ -13,14 +13,20 @@ sessions' ring stripes byte for byte against the oracle's Q4_0 restatement:
   * config 5: chunked prefill of 16 sessions x 256 bf16 tokens x 32 heads
     into a W=512 ring, with the history full (pos0 = 1024) and empty (0).
 
-K/V are generated on the GPU with a seeded torch generator; the sampled
-sessions' rows are copied back and quantized by the oracle."""
+The inputs are the configurations' seeded streams (splitmix64 + Box-Muller,
+seeds 0xB0A00003..5, bench.py's layouts), generated on the GPU by
+libbmo_synth.so exactly as bench.py generates them; the sampled sessions'
+K/V, q and positions are regenerated on the CPU from the same seeds by the
+oracle, not copied back, so the check also shows that the seeds reproduce the
+inputs."""
 import numpy as np
 import pytest
 
+import bench
 import oracle
 from _ringsim import check_close
 from bmo_jetson_amd import KVRing
+from bmo_jetson_amd.synth import positions
 
 pytestmark = pytest.mark.gpu
 
@@ -30,16 +36,6 @@ NBLK = D // 32
 
 def _i32(torch, vals):
     return torch.tensor([int(v) for v in vals], dtype=torch.int32, device="cuda")
-
-
-def _kv_rows(torch, gen, n, outliers):
-    """n rows of [H][D] K and V on the GPU, ~N(0,1), optionally x8 w.p. 1%."""
-    k = torch.randn((n, H, D), device="cuda", generator=gen)
-    v = torch.randn((n, H, D), device="cuda", generator=gen)
-    if outliers:
-        k.mul_(torch.where(torch.rand((n, H, D), device="cuda", generator=gen) < 0.01, 8.0, 1.0))
-        v.mul_(torch.where(torch.rand((n, H, D), device="cuda", generator=gen) < 0.01, 8.0, 1.0))
-    return k, v
 
 
 def _oracle_stripes(k_host, v_host, lo):
@@ -66,46 +62,56 @@ def _assert_stripes_equal(ring, layer, s, kc, vc, what):
 
 
 def _decode_config(gpu, S, fused, seed, sample):
+    """Layer 31 of a 32-layer ring filled as bench.fill_ring fills it (only
+    layer 31 is written; the other layers' stripes stay zero and unread)."""
     torch = gpu
     L, layer = 32, 31
-    rng = np.random.default_rng(seed)
-    pos = rng.integers(512, 4096, size=S)
+    pos = np.array(positions(seed, S))
+    assert pos.min() >= 512 and pos.max() < 4096
+    end = pos - (1 if fused else 0)          # the window's last position
     ring = KVRing(L, S, H, D, W)
     try:
-        gen = torch.Generator(device="cuda")
-        gen.manual_seed(seed)
+        from bmo_jetson_amd.synth import fill_normal
         stream = torch.cuda.current_stream()
-        host = {}
+        k = torch.empty((S, W, H, D), device="cuda")
+        v = torch.empty((S, W, H, D), device="cuda")
+        off = layer * S * W * H * D
+        fill_normal(k, seed, off, True, stream=stream)
+        fill_normal(v, seed + 1, off, True, stream=stream)
         for s in range(S):
-            # the window ending at pos (decode) or just before it (fused append)
-            hi = int(pos[s]) + (0 if fused else 1)
-            lo = hi - W if not fused else hi - (W - 1)
-            k, v = _kv_rows(torch, gen, hi - lo, outliers=True)
-            ring.write(layer, s, lo, k, v, stream=stream)
-            if s in sample:
-                host[s] = (lo, k.cpu().numpy(), v.cpu().numpy())
-        q = torch.randn((S, H, D), device="cuda", generator=gen)
+            ring.write(layer, s, int(end[s]) - W + 1, k[s], v[s], stream=stream)
+        del k, v
+        qoff = layer * S * H * D
+        q = torch.empty((S, H, D), device="cuda")
+        fill_normal(q, seed + 2, qoff, stream=stream)
         out = torch.full((S, H, D), float("nan"), device="cuda")
         posd = _i32(torch, pos)
         if fused:
-            kn = torch.randn((S, H, D), device="cuda", generator=gen)
-            vn = torch.randn((S, H, D), device="cuda", generator=gen)
+            kn = torch.empty((S, H, D), device="cuda")
+            vn = torch.empty((S, H, D), device="cuda")
+            fill_normal(kn, seed + 3, qoff, stream=stream)
+            fill_normal(vn, seed + 4, qoff, stream=stream)
             ring.append_decode(layer, posd, q, kn, vn, out, H, stream=stream)
         else:
             ring.decode(layer, posd, q, out, H, stream=stream)
         torch.cuda.synchronize()
         got = out.cpu().numpy()
-        qh = q.cpu().numpy()
         assert np.all(np.isfinite(got)), "non-finite output"
         for s in sample:
-            lo, kh, vh = host[s]
+            # the session's inputs regenerated on the CPU from the seeds
+            soff = off + s * W * H * D
+            kh = oracle.kv_normal(seed, W * H * D, offset=soff).reshape(W, H, D)
+            vh = oracle.kv_normal(seed + 1, W * H * D, offset=soff).reshape(W, H, D)
+            qh = oracle.normal(seed + 2, H * D, offset=qoff + s * H * D).reshape(H, D)
+            lo = int(end[s]) - W + 1
             if fused:
-                kh = np.concatenate([kh, kn[s].cpu().numpy()[None]])
-                vh = np.concatenate([vh, vn[s].cpu().numpy()[None]])
+                kn_h = oracle.normal(seed + 3, H * D, offset=qoff + s * H * D).reshape(1, H, D)
+                vn_h = oracle.normal(seed + 4, H * D, offset=qoff + s * H * D).reshape(1, H, D)
+                kh, vh = np.concatenate([kh, kn_h]), np.concatenate([vh, vn_h])
             kc, vc = _oracle_stripes(kh, vh, lo)
             what = f"{'cfg4' if fused else 'cfg3'} session {s} pos {int(pos[s])}"
             _assert_stripes_equal(ring, layer, s, kc, vc, what)
-            check_close(got[s], oracle.ring_decode_f64(kc, vc, int(pos[s]), qh[s], H), what)
+            check_close(got[s], oracle.ring_decode_f64(kc, vc, int(pos[s]), qh, H), what)
     finally:
         ring.close()
 
@@ -121,45 +127,35 @@ def test_cfg4_full_size_fused(gpu):
 @pytest.mark.parametrize("pos0", [1024, 0])
 def test_cfg5_full_size_prefill(gpu, pos0):
     torch = gpu
-    S, C = 16, 256
+    S, C, seed = 16, 256, 0xB0A00005
     sample = [0, 7, 15]
     ring = KVRing(1, S, H, D, W)
     try:
-        gen = torch.Generator(device="cuda")
-        gen.manual_seed(0xB0A00005 + pos0)
         stream = torch.cuda.current_stream()
-        hist = {}
         if pos0:
-            for s in range(S):
-                k, v = _kv_rows(torch, gen, W, outliers=False)
-                ring.write(0, s, pos0 - W, k, v, stream=stream)
-                if s in sample:
-                    hist[s] = (k.cpu().numpy(), v.cpu().numpy())
-        q = torch.randn((S, C, H, D), device="cuda", generator=gen).to(torch.bfloat16)
-        k = torch.randn((S, C, H, D), device="cuda", generator=gen).to(torch.bfloat16)
-        v = torch.randn((S, C, H, D), device="cuda", generator=gen).to(torch.bfloat16)
+            bench.fill_ring(torch, ring, 1, S, H, D, W, [pos0 - 1] * S, seed, outliers=False)
+        q, k, v = (bench.synth(torch, (S, C, H, D), seed + i).to(torch.bfloat16) for i in (2, 3, 4))
         out = torch.full((S, C, H, D), float("nan"), device="cuda")
         ring.prefill(0, torch.full((S,), pos0, dtype=torch.int32, device="cuda"), q, k, v, out, H,
                      n_tok=C, stream=stream)
         torch.cuda.synchronize()
         got = out.cpu().numpy()
         assert np.all(np.isfinite(got)), "non-finite output"
-        qf, kf, vf = (x.float().cpu().numpy() for x in (q, k, v))
+        n = C * H * D
         for s in sample:
+            qf, kf, vf = (oracle.round_bf16(oracle.normal(seed + i, n, offset=s * n)).reshape(C, H, D)
+                          for i in (2, 3, 4))
             if pos0:
-                kc, vc = _oracle_stripes(*hist[s], pos0 - W)
+                hoff = s * W * H * D
+                hist = (oracle.normal(seed, W * H * D, offset=hoff).reshape(W, H, D),
+                        oracle.normal(seed + 1, W * H * D, offset=hoff).reshape(W, H, D))
+                kc, vc = _oracle_stripes(*hist, pos0 - W)
             else:
                 kc, vc = oracle.new_ring(H, W, D)
             what = f"cfg5 pos0 {pos0} session {s}"
-            ref = oracle.ring_prefill_f64(kc, vc, pos0, qf[s], kf[s], vf[s], H)
+            ref = oracle.ring_prefill_f64(kc, vc, pos0, qf, kf, vf, H)
             check_close(got[s], ref, what)
-            # after the chunk the ring holds the chunk's blocks at its slots
-            kc2, vc2 = _oracle_stripes(kf[s], vf[s], pos0)
-            if pos0:
-                kc2h, vc2h = _oracle_stripes(*hist[s], pos0 - W)
-                keep = np.ones(W, bool)
-                keep[(pos0 + np.arange(C)) % W] = False
-                kc2[:, keep], vc2[:, keep] = kc2h[:, keep], vc2h[:, keep]
-            _assert_stripes_equal(ring, 0, s, kc2, vc2, what)
+            # (the oracle's prefill appended the chunk to kc, vc)
+            _assert_stripes_equal(ring, 0, s, kc, vc, what)
     finally:
         ring.close()
