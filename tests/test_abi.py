@@ -87,3 +87,24 @@ def test_package_fails_loudly_without_library(tmp_path, monkeypatch):
     monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "missing.so"))
     with pytest.raises(RuntimeError, match="no CPU fallback"):
         _lib.lib()
+
+
+def test_synth_header_symbols_exported():
+    """libbmo_synth.so (the benchmark inputs' generator) exports exactly what
+    include/bmo_synth.h declares, and rejects a bad length without launching."""
+    import os
+    import re
+    from bmo_jetson_amd import synth
+    text = open(os.path.join(_lib.ROOT, "include", "bmo_synth.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    text = "\n".join(l for l in text.splitlines() if not l.lstrip().startswith("#"))
+    names = set(re.findall(r"BMO_SYNTH_API\s+[^;(]*?\b(\w+)\s*\(", text))
+    assert names == {"bmo_synth_fill_normal"}
+    out = subprocess.run(["nm", "-D", "--defined-only", synth.SYNTH_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    assert {s for s in exported if s.startswith("bmo")} == names
+    L = synth.lib()
+    assert L.bmo_synth_fill_normal(None, -1, 0, 0, 0, None) == 2
+    assert L.bmo_synth_fill_normal(None, 5, 0, 0, 0, None) == 2
+    assert L.bmo_synth_fill_normal(None, 0, 0, 0, 0, None) == 0
