@@ -2,9 +2,12 @@
 // include/bmo_attn.h alone (the HIP runtime only for its device buffers), the
 // way the reference's C++ engine drives its attention node: a two-layer ring
 // with two sessions, a per-session handle on session 1, and token steps at
-// consecutive positions that wrap the ring -- first eager
-// (bmo_attn_session_forward), then from the captured graph
-// (bmo_attn_session_capture / bmo_attn_session_replay) -- with and without
+// consecutive positions that wrap the ring -- eager whole steps
+// (bmo_attn_session_forward), replays of a captured step
+// (bmo_attn_session_capture / _replay), eager steps one layer at a time
+// (bmo_attn_session_begin_step / _layer / _end_step / _sync, the calls a
+// model's layer loop makes between its own kernels), and replays of such a
+// step captured by bmo_attn_session_capture_begin / _end -- with and without
 // RoPE.  After every step each layer's output is checked against the CPU
 // oracle (oracle/liboracle.so, test infrastructure) at
 // |gpu - ref| <= 2e-3 + 1e-3 |ref|; at the end the ring's blocks of both
@@ -24,7 +27,9 @@
 namespace {
 
 constexpr int kLayers = 2, kSessions = 2, kSession = 1, kHeads = 8, kKv = 4, kD = 128, kCtx = 48;
-constexpr int kSteps = 60, kEagerSteps = 25;
+// steps [0, 25) forward, [25, 45) replays of a captured step, [45, 52)
+// layer by layer, [52, 75) replays of a step captured layer by layer
+constexpr int kSteps = 75, kEagerSteps = 25, kReplayEnd = 45, kLayerEnd = 52;
 constexpr int kBlocks = kD / 32;
 
 bool hip_ok(hipError_t e, const char *what) {
@@ -71,13 +76,40 @@ int run(float theta) {
             !hip_ok(hipMemcpy(k, hk.data(), kn * 4, hipMemcpyHostToDevice), "hipMemcpy") ||
             !hip_ok(hipMemcpy(v, hv.data(), kn * 4, hipMemcpyHostToDevice), "hipMemcpy"))
             return 1;
-        int rc;
+        // one layer's q/k/v/out inside the step's buffers
+        auto layer_call = [&](int l) {
+            return bmo_attn_session_layer(s, l, q + (size_t) l * kHeads * kD, k + (size_t) l * kKv * kD,
+                                          v + (size_t) l * kKv * kD, out + (size_t) l * kHeads * kD);
+        };
+        int rc = BMO_ATTN_OK;
         if (p < kEagerSteps) {
             rc = bmo_attn_session_forward(s, p, q, k, v, out);
-        } else {
+        } else if (p < kReplayEnd) {
             if (p == kEagerSteps && (rc = bmo_attn_session_capture(s, q, k, v, out)) != BMO_ATTN_OK) {
                 std::printf("FAIL capture: %s\n", bmo_attn_session_last_error(s));
                 return 1;
+            }
+            rc = bmo_attn_session_replay(s, p);
+        } else if (p < kLayerEnd) {
+            rc = bmo_attn_session_begin_step(s, p);
+            for (int l = kLayers - 1; l >= 0 && rc == BMO_ATTN_OK; --l) rc = layer_call(l);  // any order
+            if (rc == BMO_ATTN_OK) rc = bmo_attn_session_end_step(s);
+            if (rc == BMO_ATTN_OK) rc = bmo_attn_session_sync(s);
+        } else {
+            if (p == kLayerEnd) {
+                rc = bmo_attn_session_capture_begin(s);
+                for (int l = 0; l < kLayers && rc == BMO_ATTN_OK; ++l) rc = layer_call(l);
+                if (rc == BMO_ATTN_OK) rc = bmo_attn_session_end_step(s);
+                const int rc_end = bmo_attn_session_capture_end(s);
+                if (rc != BMO_ATTN_OK || rc_end != BMO_ATTN_OK) {
+                    std::printf("FAIL layer capture: %s\n", bmo_attn_session_last_error(s));
+                    return 1;
+                }
+                if (bmo_attn_session_pos(s) != p) {
+                    std::printf("FAIL layer capture moved the position to %lld\n",
+                                (long long) bmo_attn_session_pos(s));
+                    return 1;
+                }
             }
             rc = bmo_attn_session_replay(s, p);
         }
@@ -147,8 +179,10 @@ int run(float theta) {
     bmo_attn_session_free(s);
     bmo_kv_ring_free(ring);
     if (!fails)
-        std::printf("ok theta %g: %d steps (%d eager, %d graph replays), %ld values checked, ring bit-exact\n",
-                    theta, kSteps, kEagerSteps, kSteps - kEagerSteps, checked);
+        std::printf("ok theta %g: %d steps (%d eager, %d replays of a captured step, %d layer by layer, %d "
+                    "replays of a step captured layer by layer), %ld values checked, ring bit-exact\n",
+                    theta, kSteps, kEagerSteps, kReplayEnd - kEagerSteps, kLayerEnd - kReplayEnd,
+                    kSteps - kLayerEnd, checked);
     return fails;
 }
 
