@@ -47,6 +47,14 @@ def _run(gpu, rows, cols, x, seed, scratch=True):
     (4096, 5632),    # gating linear out (reference bench shape)
     (37, 11264),     # three pair iterations per lane, rows not a multiple of 32
     (1, 64),
+    (16383, 4096),   # four two-row chunks per wave of the streaming kernel, odd rows
+    (6001, 2048),    # waves with fewer chunks than others, a one-row last chunk
+    (3, 192),        # three pairs per row: lanes past them idle
+    (2049, 4096),    # one workgroup more than a round of chunks
+    (16385, 4096),   # beyond four chunks per wave: the pair-walking kernel
+    (8191, 5632),    # two 7-piece chunks per wave, two pairs per lane, odd rows
+    (4096, 6144),    # the widest rows the streaming kernel takes
+    (64, 4352),      # 4096 < cols: lanes past the row's 68 pairs idle in the second pass
 ])
 def test_gemv_shapes(gpu, rows, cols):
     _run(gpu, rows, cols, oracle.normal(7 + cols, cols), seed=rows)
