@@ -410,10 +410,33 @@ def bench_gemv(torch, reps=50):
             call(torch.cuda.current_stream())
         torch.cuda.synchronize()
         us = graph_us_per_call(torch, call, max(reps, n_copies))
+        # the read probe over the same weight copies: one launch's ceiling
+        ceil = read_ceiling(torch, [w[i].data_ptr() for i in range(n_copies)], nbytes, reps)
         del w
         res[name] = {"us": round(us, 3), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
-                     "hbm_frac": round(nbytes / (us * 1e-6) / 8e12, 4), "weight_bytes": nbytes}
+                     "hbm_frac": round(nbytes / (us * 1e-6) / 8e12, 4), "weight_bytes": nbytes,
+                     "read_probe_us": ceil["us_per_launch"]}
     return res
+
+
+def read_ceiling(torch, ptrs, nbytes, reps=20):
+    """The read probe of libbmo_synth.so (one 16-byte nontemporal load per
+    thread, the fastest single-pass read pattern measured) over the buffers
+    at device addresses ptrs, nbytes each, one launch per buffer in turn,
+    timed like a kernel leg (graph replays): the ceiling for one launch that
+    reads those bytes once."""
+    from bmo_jetson_amd.synth import read_probe
+
+    sink = torch.zeros(256, dtype=torch.int32, device="cuda")
+    state = {"i": 0}
+
+    def call(st):
+        read_probe(ptrs[state["i"] % len(ptrs)], nbytes, sink, stream=st)
+        state["i"] += 1
+
+    us = graph_us_per_call(torch, call, max(reps, len(ptrs)))
+    return {"bytes_per_launch": nbytes, "us_per_launch": round(us, 3),
+            "GBps": round(nbytes / (us * 1e-6) / 1e9, 1), "hbm_frac": round(nbytes / (us * 1e-6) / 8e12, 4)}
 
 
 def run_decode(torch, config, steps, warmup, sessions=None):
@@ -647,6 +670,16 @@ def main():
         "hbm_frac": run["hbm_frac"],
         "roofline": run["roofline"],
     }
+    # the read probe over each layer's ring stripes (the window bytes the
+    # decode launch of that layer reads; q and out, 1 MB each at cfg3, are
+    # not in it): the ceiling of one launch
+    ring0 = run["ring"]
+    slice_bytes = ring0.nbytes // L
+    result["read_ceiling"] = read_ceiling(torch, [ring0.k_base + i * slice_bytes for i in range(L)],
+                                          slice_bytes)
+    result["read_ceiling"]["note"] = ("libbmo_synth.so read probe over one layer's ring stripes per launch, "
+                                      "32 launches per graph; compare the decode's launch_us")
+    log(f"[bench] read ceiling: {result['read_ceiling']}")
     if args.config == "cfg3" and not args.no_cfg4:
         # BASELINE config 4 (fused append + decode, 256 sessions) at the same
         # step count; its 19.3 GB ring is freed before the other legs

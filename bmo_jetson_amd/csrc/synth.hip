@@ -1,6 +1,6 @@
-// synth.hip -- the device generator of include/bmo_synth.h: the seeded
-// synthetic inputs of the benchmark configurations, bit for bit the stream
-// the CPU restates.  Every floating-point step is an IEEE double add,
+// synth.hip -- the device side of include/bmo_synth.h: the seeded synthetic
+// inputs of the benchmark configurations, bit for bit the stream the CPU
+// restates, and the benchmark's read probe.  Every floating-point step is an IEEE double add,
 // subtract, multiply, divide or square root (correctly rounded on gfx950 as
 // on the host), the build contracts none of them (-ffp-contract=off), and
 // the integer steps are exact, so each element is a pure function of
@@ -108,5 +108,34 @@ extern "C" int bmo_synth_fill_normal(float *out, int64_t n, uint64_t seed, uint6
     const unsigned grid = (unsigned) (blocks < 65536 ? blocks : 65536);
     hipLaunchKernelGGL(fill_kernel, dim3(grid), dim3(256), 0, (hipStream_t) stream, out, n, seed, offset,
                        outliers);
+    return hipGetLastError() == hipSuccess ? 0 : 8;
+}
+
+namespace {
+
+typedef unsigned int probe_u32x4 __attribute__((ext_vector_type(4)));
+
+// One 16-byte nontemporal load per thread: piece i of the buffer is read by
+// thread i once, and a workgroup retires as soon as its loads return.  The
+// xor test keeps the loads (its store fires only for one value in 2^32).
+__global__ __launch_bounds__(256) void read_probe_kernel(const probe_u32x4 *src, int64_t n16, uint32_t *sink) {
+    const int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x;
+    if (i >= n16) return;
+    const probe_u32x4 v = __builtin_nontemporal_load(src + i);
+    if ((v.x ^ v.y ^ v.z ^ v.w) == 0x9E3779B9u) sink[threadIdx.x] = 1u;
+}
+
+}  // namespace
+
+extern "C" int bmo_synth_read_probe(const void *buf, int64_t bytes, uint32_t *sink, void *stream) {
+    if (bytes < 0 || bytes % 16 != 0 || (bytes > 0 && (!buf || !sink)) ||
+        (reinterpret_cast<uintptr_t>(buf) & 15) != 0)
+        return 2;
+    if (bytes == 0) return 0;
+    const int64_t n16 = bytes / 16;
+    const int64_t blocks = (n16 + 255) / 256;
+    if (blocks > 0x7FFFFFFF) return 2;
+    hipLaunchKernelGGL(read_probe_kernel, dim3((unsigned) blocks), dim3(256), 0, (hipStream_t) stream,
+                       reinterpret_cast<const probe_u32x4 *>(buf), n16, sink);
     return hipGetLastError() == hipSuccess ? 0 : 8;
 }

@@ -1,5 +1,6 @@
 """ctypes binding of libbmo_synth.so (include/bmo_synth.h): the seeded
-synthetic inputs of the benchmark configurations, generated on the GPU.
+synthetic inputs of the benchmark configurations, generated on the GPU, and
+the benchmark's read probe.
 Element c of stream `seed` is a splitmix64 + Box-Muller normal; with
 ``outliers`` it is multiplied by 8 with probability 1% (configurations 3 and
 4).  The CPU restatement is the oracle's (test infrastructure); the two agree
@@ -25,6 +26,8 @@ def lib() -> ctypes.CDLL:
         L.bmo_synth_fill_normal.restype = ctypes.c_int
         L.bmo_synth_fill_normal.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_uint64,
                                             ctypes.c_uint64, ctypes.c_int, ctypes.c_void_p]
+        L.bmo_synth_read_probe.restype = ctypes.c_int
+        L.bmo_synth_read_probe.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p]
         _lib = L
     return _lib
 
@@ -38,6 +41,17 @@ def fill_normal(out, seed: int, offset: int = 0, outliers: bool = False, stream=
                                      offset & (2**64 - 1), 1 if outliers else 0, _stream(stream))
     if rc != 0:
         raise RuntimeError(f"bmo_synth_fill_normal failed with code {rc}")
+
+
+def read_probe(ptr: int, nbytes: int, sink, stream=None) -> None:
+    """One pass of the read probe over nbytes of device memory at address
+    ptr (16-byte aligned, nbytes a multiple of 16); sink is a device tensor
+    of at least 1 KiB."""
+    from .ring import _stream
+    assert sink.is_cuda and sink.numel() * sink.element_size() >= 1024
+    rc = lib().bmo_synth_read_probe(ptr, nbytes, sink.data_ptr(), _stream(stream))
+    if rc != 0:
+        raise RuntimeError(f"bmo_synth_read_probe failed with code {rc}")
 
 
 _M64 = (1 << 64) - 1

@@ -1,10 +1,11 @@
 /*
- * bmo_synth.h -- device generator of the synthetic inputs of the benchmark
- * configurations (libbmo_synth.so).  Not part of the attention ABI
- * (bmo_attn.h) and with no counterpart in the reference: it exists so that
- * the benchmark and the full-size tests draw their q/k/v from the seeded
- * stream the configurations name, on the GPU, and the CPU can regenerate any
- * part of them.
+ * bmo_synth.h -- benchmark support (libbmo_synth.so): the device generator of
+ * the synthetic inputs of the benchmark configurations, and a read probe.
+ * Not part of the attention ABI (bmo_attn.h) and with no counterpart in the
+ * reference: the generator exists so that the benchmark and the full-size
+ * tests draw their q/k/v from the seeded stream the configurations name, on
+ * the GPU, and the CPU can regenerate any part of them; the probe states the
+ * memory ceiling of a single pass over the bytes a kernel reads.
  *
  * Stream: element c of stream `seed` is a Box-Muller normal of two
  * splitmix64 words (Steele, Lea, Flood 2014), cosine branch only:
@@ -42,6 +43,16 @@ extern "C" {
  * or a NULL out with n > 0, 8 for a HIP launch error. */
 BMO_SYNTH_API int bmo_synth_fill_normal(float *out, int64_t n, uint64_t seed, uint64_t offset,
                                         int outliers, void *stream);
+
+/* Reads `bytes` of device memory at buf once, asynchronously on stream, with
+ * one 16-byte nontemporal load per thread in workgroups of 256 (of the read
+ * patterns measured on MI355X, the fastest single pass), and discards the
+ * data: the time of this launch is the ceiling for a kernel that reads the
+ * same bytes in one launch.  sink: device memory of at least 1 KiB, written
+ * only for one value in 2^32 of a piece's xor.  Returns 0, 2 for bytes < 0,
+ * bytes not a multiple of 16, buf not 16-byte aligned or a NULL pointer with
+ * bytes > 0, 8 for a HIP launch error. */
+BMO_SYNTH_API int bmo_synth_read_probe(const void *buf, int64_t bytes, uint32_t *sink, void *stream);
 
 #ifdef __cplusplus
 }

@@ -90,8 +90,9 @@ def test_package_fails_loudly_without_library(tmp_path, monkeypatch):
 
 
 def test_synth_header_symbols_exported():
-    """libbmo_synth.so (the benchmark inputs' generator) exports exactly what
-    include/bmo_synth.h declares, and rejects a bad length without launching."""
+    """libbmo_synth.so (the benchmark inputs' generator and read probe)
+    exports exactly what include/bmo_synth.h declares, and rejects bad
+    arguments without launching."""
     import os
     import re
     from bmo_jetson_amd import synth
@@ -99,7 +100,7 @@ def test_synth_header_symbols_exported():
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     text = "\n".join(l for l in text.splitlines() if not l.lstrip().startswith("#"))
     names = set(re.findall(r"BMO_SYNTH_API\s+[^;(]*?\b(\w+)\s*\(", text))
-    assert names == {"bmo_synth_fill_normal"}
+    assert names == {"bmo_synth_fill_normal", "bmo_synth_read_probe"}
     out = subprocess.run(["nm", "-D", "--defined-only", synth.SYNTH_PATH], capture_output=True,
                          text=True, check=True).stdout
     exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
@@ -108,3 +109,8 @@ def test_synth_header_symbols_exported():
     assert L.bmo_synth_fill_normal(None, -1, 0, 0, 0, None) == 2
     assert L.bmo_synth_fill_normal(None, 5, 0, 0, 0, None) == 2
     assert L.bmo_synth_fill_normal(None, 0, 0, 0, 0, None) == 0
+    assert L.bmo_synth_read_probe(None, -16, None, None) == 2
+    assert L.bmo_synth_read_probe(None, 16, None, None) == 2           # NULL buffer
+    assert L.bmo_synth_read_probe(ctypes.c_void_p(16), 24, ctypes.c_void_p(16), None) == 2  # not whole pieces
+    assert L.bmo_synth_read_probe(ctypes.c_void_p(8), 16, ctypes.c_void_p(16), None) == 2   # misaligned
+    assert L.bmo_synth_read_probe(None, 0, None, None) == 0
