@@ -124,23 +124,36 @@ float f16_to_f32_host(uint16_t h) {
 
 // Copies the groups holding slots [t0, t0+n) of one stripe to host, packed
 // back to back; *first receives the first group's index.
+// (One 1-D copy per group rather than one strided hipMemcpy2D: under
+// rocprofv3's kernel trace, hipMemcpy2D device-to-host returned wrong bytes
+// for these strides on MI355X while 1-D copies of the same groups were
+// exact.  These are the host-side readout paths, not the hot path.)
 hipError_t fetch_groups(const bmo_kv_ring_t *r, const uint8_t *stripe, int t0, int n,
                         std::vector<uint8_t> &buf, int *first) {
     const int G = bmo::keys_per_group(r->g.head_dim);
     const int g0 = t0 / G, g1 = (t0 + n - 1) / G;
     *first = g0;
     buf.resize((size_t) (g1 - g0 + 1) * bmo::kGroupBytes);
-    return hipMemcpy2D(buf.data(), bmo::kGroupBytes, stripe + (int64_t) g0 * r->g.group_stride,
-                       (size_t) r->g.group_stride, bmo::kGroupBytes, (size_t) (g1 - g0 + 1),
-                       hipMemcpyDeviceToHost);
+    for (int g = g0; g <= g1; ++g) {
+        const hipError_t e = hipMemcpy(buf.data() + (size_t) (g - g0) * bmo::kGroupBytes,
+                                       stripe + (int64_t) g * r->g.group_stride, bmo::kGroupBytes,
+                                       hipMemcpyDeviceToHost);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 // Writes packed groups back to their places in a stripe.
 hipError_t store_groups(const bmo_kv_ring_t *r, uint8_t *stripe, const std::vector<uint8_t> &buf,
                         int first) {
-    return hipMemcpy2D(stripe + (int64_t) first * r->g.group_stride, (size_t) r->g.group_stride,
-                       buf.data(), bmo::kGroupBytes, bmo::kGroupBytes,
-                       buf.size() / bmo::kGroupBytes, hipMemcpyHostToDevice);
+    const size_t n = buf.size() / bmo::kGroupBytes;
+    for (size_t i = 0; i < n; ++i) {
+        const hipError_t e = hipMemcpy(stripe + (int64_t) (first + (int64_t) i) * r->g.group_stride,
+                                       buf.data() + i * bmo::kGroupBytes, bmo::kGroupBytes,
+                                       hipMemcpyHostToDevice);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 // ggml block (scale bits, 16 code bytes) of K (which 0) or V (which 1) at
