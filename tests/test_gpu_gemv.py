@@ -85,3 +85,35 @@ def test_gemv_without_scratch_and_errors(gpu):
     assert L.bmo_launch_gemv_q4_0_q8_1(p, off, p, 4, 64, None, None) == 2
     assert L.bmo_launch_gemv_q4_0_q8_1(p, p, p, 4, 65536, None, None) == 2
     gpu.cuda.synchronize()
+
+
+def _launch(gpu, wbytes, w_off, x, rows, cols):
+    """y from a weight matrix placed w_off bytes into its device buffer."""
+    wd = gpu.zeros(wbytes.size + 64, dtype=gpu.uint8, device="cuda")
+    wd[w_off:w_off + wbytes.size] = gpu.from_numpy(wbytes).cuda()
+    xd = gpu.from_numpy(np.ascontiguousarray(x, dtype=np.float32)).cuda()
+    y = gpu.full((rows,), float("nan"), dtype=gpu.float32, device="cuda")
+    rc = _lib.lib().bmo_launch_gemv_q4_0_q8_1(ctypes.c_void_p(wd.data_ptr() + w_off), _ptr(xd), _ptr(y),
+                                              rows, cols, None, None)
+    assert rc == 0
+    gpu.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+@pytest.mark.parametrize("rows,cols", [(12288, 4096), (4095, 5632), (2049, 1024)])
+def test_gemv_kernels_agree_bitwise(gpu, monkeypatch, rows, cols):
+    """The streaming kernel and the pair-walking kernel share the quantizer
+    and the pair product, so their outputs are equal bit for bit: a matrix
+    at a 16-byte aligned address takes the streaming kernel, the same matrix
+    4 bytes further (or BMO_GEMV_STREAM=0) the pair-walking one."""
+    w = oracle.quantize_q4_0(oracle.normal(rows + cols, rows * cols)).view(np.uint8).copy()
+    x = oracle.normal(31 + cols, cols)
+    a = _launch(gpu, w, 0, x, rows, cols)
+    b = _launch(gpu, w, 4, x, rows, cols)
+    monkeypatch.setenv("BMO_GEMV_STREAM", "0")
+    c = _launch(gpu, w, 0, x, rows, cols)
+    assert np.all(np.isfinite(a))
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert np.array_equal(a.view(np.uint32), c.view(np.uint32))
+    ref, tabs = oracle.gemv_q4_0_q8_1_f64(w.view(oracle.BLOCK_DTYPE), oracle.quantize_q8_1(x), rows, cols)
+    assert np.all(np.abs(a - ref) <= 1e-5 * tabs + 1e-6)
