@@ -429,8 +429,9 @@ BMO_ATTN_API const char *bmo_attn_session_last_error(bmo_attn_session_t *s);
  * of 64 (at most 52428); W_dev and q8_scratch 4-byte aligned, x_dev 16-byte
  * aligned.  A 16-byte aligned W_dev with cols a multiple of 256, at most 6144,
  * and at most 16384 rows takes a faster streaming kernel; the outputs are
- * the same bit for bit either way.  Asynchronous on stream.  Returns BMO_ATTN_OK or an error code;
- * rejected arguments launch nothing and are reported once on stderr (the
+ * the same bit for bit either way.  Asynchronous on stream.  Returns
+ * BMO_ATTN_OK or an error code; rejected arguments launch nothing and are
+ * reported once on stderr (the
  * reference's launcher returns nothing). */
 BMO_ATTN_API int bmo_launch_gemv_q4_0_q8_1(const void *W_dev, const float *x_dev,
                                            float *y_dev, int rows, int cols,
