@@ -431,8 +431,7 @@ BMO_ATTN_API const char *bmo_attn_session_last_error(bmo_attn_session_t *s);
  * and at most 16384 rows takes a faster streaming kernel; the outputs are
  * the same bit for bit either way.  Asynchronous on stream.  Returns
  * BMO_ATTN_OK or an error code; rejected arguments launch nothing and are
- * reported once on stderr (the
- * reference's launcher returns nothing). */
+ * reported once on stderr (the reference's launcher returns nothing). */
 BMO_ATTN_API int bmo_launch_gemv_q4_0_q8_1(const void *W_dev, const float *x_dev,
                                            float *y_dev, int rows, int cols,
                                            void *q8_scratch, void *stream);
