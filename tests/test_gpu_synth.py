@@ -38,3 +38,21 @@ def test_synth_grid_stride(gpu):
     got = out.cpu().numpy()
     tail = oracle.kv_normal(0xB0A00003, 3000, offset=99 + n - 3000)
     assert np.array_equal(got[-3000:].view(np.uint32), tail.view(np.uint32))
+
+
+def test_read_probe_reads_and_leaves_data(gpu):
+    """The bench's read probe (bmo_synth_read_probe) runs over a buffer, on a
+    stream, without changing it; its sink is written only when a 16-byte
+    piece's xor is 0x9E3779B9, which one planted piece makes happen."""
+    from bmo_jetson_amd.synth import read_probe
+    n = (1 << 20) + 16                       # not a multiple of the workgroup's 4 KiB
+    buf = gpu.zeros(n // 4, dtype=gpu.int32, device="cuda")
+    buf[4:8] = gpu.tensor([0x9E3779B9 - (1 << 32), 0, 0, 0], dtype=gpu.int32)  # piece 1
+    before = buf.cpu().numpy().copy()
+    sink = gpu.zeros(256, dtype=gpu.int32, device="cuda")
+    st = gpu.cuda.Stream()
+    read_probe(buf.data_ptr(), n, sink, stream=st)
+    st.synchronize()
+    assert np.array_equal(buf.cpu().numpy(), before)
+    got = sink.cpu().numpy()
+    assert got[1] == 1 and np.count_nonzero(got) == 1    # piece 1 is read by thread 1
