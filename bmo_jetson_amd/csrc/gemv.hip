@@ -285,10 +285,10 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvParams p) {
 
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
-// Streaming variant for rows of at most 64 block pairs whose byte length
-// is a multiple of 16 (cols <= 4096, a multiple of 256).  A
-// wave owns up to NPOS chunks of two consecutive rows (c0, c0 + stride, ...),
-// at most 4608 contiguous bytes each.  Lane l loads the chunk's 16-byte
+// Streaming variant for rows whose byte length is a multiple of 16 (cols a
+// multiple of 256, at most 6144).  A wave owns up to NPOS chunks of two
+// consecutive rows (c0, c0 + stride, ...), at most NPC KiB of contiguous
+// bytes each (4608 bytes at 4096 columns).  Lane l loads the chunk's 16-byte
 // pieces j * 1024 + 16 l with nontemporal loads (every byte is loaded once,
 // by one lane), the wave copies the chunk into its own LDS area and each
 // lane reads its block pair from there.  One chunk is in flight at a time:
