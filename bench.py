@@ -374,6 +374,86 @@ def bench_prefill(torch, reps=10):
     return res
 
 
+def prefill_phases(torch, reps=10):
+    """Phase timings of the cfg5 prefill kernel from the diagnostic library
+    libbmo_attn_phases.so (its prefill kernel records s_memtime at each
+    phase boundary of every wave; see prefill.hip).  Per case the calls run
+    as the prefill leg times them (graph replays after warm-up), and the last
+    call's stamps are read; the summary gives medians over the
+    workgroups of each round of 256 (the rounds cannot overlap: one workgroup
+    fills a CU) and over the barrier periods of the tile loop, in us, and the
+    instrumented calls' duration.  Run in its own process: it loads the
+    diagnostic library in place of libbmo_attn.so."""
+    import ctypes
+    from bmo_jetson_amd import KVRing, _lib
+
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    lib.bmo_prefill_phase_stamps.restype = ctypes.c_int
+    lib.bmo_prefill_phase_stamps.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    S, C, W, H, D, seed = 16, 256, 512, 32, 128, 0xB0A00005
+    NWG, NW, REC = 512, 16, 128
+    res = {"workload": "cfg5, one layer per call; medians over workgroups (per round) and periods",
+           "library": os.path.basename(_lib.LIB_PATH)}
+    for name, p0 in (("full", 1024), ("empty", 0)):
+        ring = KVRing(1, S, H, D, W)
+        if p0:
+            fill_ring(torch, ring, 1, S, H, D, W, [p0 - 1] * S, seed, outliers=False)
+        q, k, v = (synth(torch, (S, C, H, D), seed + i).to(torch.bfloat16) for i in (2, 3, 4))
+        out = torch.empty((S, C, H, D), device="cuda")
+        pos0 = torch.full((S,), p0, dtype=torch.int32, device="cuda")
+        call = lambda st: ring.prefill(0, pos0, q, k, v, out, H, n_tok=C, stream=st)
+        for _ in range(3):
+            call(torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        # graph replays as in the prefill leg (warm clocks); the stamps are
+        # those of the last call replayed
+        call_us = graph_us_per_call(torch, call, reps)
+        a = np.zeros(NWG * NW * REC, dtype=np.uint64)
+        assert lib.bmo_prefill_phase_stamps(a.ctypes.data, a.nbytes) == 0
+        ring.close()
+        a = a.astype(np.int64).reshape(NWG, NW, REC)
+        ticks_per_us = np.median((a[:, :, 6] - a[:, :, 1]) / ((a[:, :, 7] - a[:, :, 0]) / 100.0))
+        us = lambda x: x / ticks_per_us
+        start = (a[:, :, 0].min(1) - a[:, :, 0].min()) / 100.0  # real-time clock: 100 MHz
+        first = start < np.median(start)
+        case = {"p0": p0, "call_us": round(call_us, 2),
+                "kernel_span_us": round((a[:, :, 7].max() - a[:, :, 0].min()) / 100.0, 2),
+                "shader_clock_GHz": round(ticks_per_us / 1000.0, 3)}
+        for rname, sel in (("round1", first), ("round2", ~first)):
+            b = a[sel]
+            case[rname] = {
+                "workgroups": int(sel.sum()),
+                "start_us": round(float(np.median(start[sel])), 2),
+                "query_rows_converted_us": round(float(np.median(us(b[:, :, 2] - b[:, :, 1]))), 2),
+                "chunk_quantized_us": round(float(np.median(us(b[:, :, 3] - b[:, :, 2]))), 2),
+                "loop_us": round(float(np.median(us(b[:, :, 5] - b[:, :, 4]))), 2),
+                "epilogue_us": round(float(np.median(us(b[:, :, 6] - b[:, :, 5]))), 2),
+            }
+        n = int(np.median(a[:, :, 8]))
+        P = min(n, REC - 16) // 4
+        per = a[:, :, 16:16 + 4 * P].reshape(NWG, NW, P, 4)
+        A, B, Cd, Dd = (per[..., i] for i in range(4))
+        nxt = np.concatenate([A[:, :, 1:], a[:, :, 5:6]], axis=2)
+        loaders = slice(0, NW // 2)
+        others = slice(NW // 2, NW)
+        med = lambda x: round(float(np.median(x)), 3)
+        case["periods"] = P
+        case["period_us"] = med(us(nxt[:, 0] - A[:, 0]))
+        case["loading_waves"] = {"dequantize_us": med(us(B - A)[:, loaders]),
+                                 "barrier_wait_us": med(us(Cd - B)[:, loaders]),
+                                 "multiply_us": med(us(nxt - Dd)[:, loaders])}
+        case["other_waves"] = {"barrier_wait_us": med(us(Cd - B)[:, others]),
+                               "ring_writes_us": med(us(Dd - Cd)[:, others]),
+                               "multiply_us": med(us(nxt - Dd)[:, others])}
+        mult = us(nxt - Dd).sum(2)  # per wave, over the loop
+        case["multiply_total_us_by_wave_age"] = [round(float(np.median(mult[:, 4 * g:4 * g + 4])), 2)
+                                                 for g in range(4)]
+        case["multiply_total_us_by_wave_age_note"] = ("waves 4g .. 4g + 3: the (g+1)-th wave of each SIMD "
+                                                      "(wave w runs on SIMD w mod 4), oldest first")
+        res[name] = case
+    return res
+
+
 def bench_gemv(torch, reps=50):
     """The Q4_0 x Q8_1 GEMV of the projections around attention, at the
     reference's bench shapes (src/bmo_kernel_bench.cu:387-389) and the output
@@ -612,6 +692,9 @@ def main():
                     help="only run the cfg5 chunked-prefill leg and print its JSON (profiling)")
     ap.add_argument("--latency-only", action="store_true",
                     help="only run the B=1 and depformer legs (rocprof of the latency kernels)")
+    ap.add_argument("--prefill-phases", action="store_true",
+                    help="only run the cfg5 prefill phase timings of the diagnostic library "
+                         "libbmo_attn_phases.so and print their JSON")
     ap.add_argument("--gemv-only", action="store_true",
                     help="only run the Q4_0 GEMV leg and print its JSON (profiling)")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
@@ -640,6 +723,11 @@ def main():
         print(json.dumps({"copy_bytes_read": n * 4, "copy_bytes_written": n * 4}))
         return
 
+    if args.prefill_phases:
+        from bmo_jetson_amd import _lib
+        _lib.LIB_PATH = os.path.join(_lib.PKG_DIR, "libbmo_attn_phases.so")
+        print(json.dumps({"prefill_phases": prefill_phases(torch)}), flush=True)
+        return
     if args.prefill_only:
         print(json.dumps({"prefill": bench_prefill(torch)}), flush=True)
         return

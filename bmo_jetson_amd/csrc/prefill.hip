@@ -252,6 +252,48 @@ __global__ __launch_bounds__(256) void commit_kernel(PrefillParams p) {
 // reads the chunk's keys from there, and writes the chunk's blocks into the
 // ring during the tile loop, each once no wave reads its slot's old contents
 // from memory any more; no stage or commit kernel runs.
+// Phase timestamps, in a diagnostic build only (BMO_PREFILL_PHASES=1,
+// libbmo_attn_phases.so, which bench.py --prefill-phases reads): lane 0 of
+// every wave of the first 512 workgroups records s_memtime at its phase
+// boundaries, plus s_memrealtime at its start and end, into a device array:
+// record [0] real-time start, [1] start, [2] query rows converted, [3] chunk
+// quantized and published (DIRECT), [4] loop start, [5] loop end, [6] end,
+// [7] real-time end, [8] the number of loop stamps; loop stamps from [16]
+// on, four per barrier period: the iteration's start, arrival at the
+// barrier, departure, and the end of the ring writes (DIRECT waves without
+// items).  Scheduling barriers keep the compiler from moving work across a
+// stamp.  The normal build compiles none of it.
+#ifndef BMO_PREFILL_PHASES
+#define BMO_PREFILL_PHASES 0
+#endif
+#if BMO_PREFILL_PHASES
+constexpr int kPhaseUnits = 512;
+constexpr int kPhaseRec = 128;
+__device__ uint64_t g_prefill_phases[kPhaseUnits * 16 * kPhaseRec];
+#define BMO_PHASE(i)                                                           \
+    do {                                                                       \
+        __builtin_amdgcn_sched_barrier(0);                                     \
+        const uint64_t t_ = __builtin_amdgcn_s_memtime();                      \
+        __builtin_amdgcn_sched_barrier(0);                                     \
+        if (lane == 0) phase_rec[i] = t_;                                      \
+    } while (0)
+#define BMO_PHASE_LOOP()                                                       \
+    do {                                                                       \
+        __builtin_amdgcn_sched_barrier(0);                                     \
+        const uint64_t t_ = __builtin_amdgcn_s_memtime();                      \
+        __builtin_amdgcn_sched_barrier(0);                                     \
+        if (lane == 0 && phase_n < kPhaseRec - 16) phase_rec[16 + phase_n] = t_; \
+        ++phase_n;                                                             \
+    } while (0)
+#else
+#define BMO_PHASE(i) \
+    do {             \
+    } while (0)
+#define BMO_PHASE_LOOP() \
+    do {                 \
+    } while (0)
+#endif
+
 template <int D, int QW, int QB, bool DIRECT, bool ALIGNED>
 __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams p) {
     static_assert(!DIRECT || ALIGNED, "the direct path serves rings of a multiple of 32 slots");
@@ -306,6 +348,12 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
     // wave-uniform (readfirstlane), so that everything derived from it --
     // the tile skip, the whole-tile test -- is a scalar branch
     const int wave = __builtin_amdgcn_readfirstlane((int) threadIdx.x >> 6);
+#if BMO_PREFILL_PHASES
+    uint64_t *const phase_rec = g_prefill_phases + ((size_t) (blockIdx.x % kPhaseUnits) * QW + wave) * kPhaseRec;
+    int phase_n = 0;
+    if (lane == 0) phase_rec[0] = __builtin_amdgcn_s_memrealtime();
+    BMO_PHASE(1);
+#endif
     // (scalars: the divisions run on the vector unit, readfirstlane keeps
     // their results, and the addresses derived from them, in SGPRs)
     const int n_qt = (p.n_tok + QT - 1) / QT;
@@ -614,6 +662,7 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
 #pragma unroll
             for (int r = 0; r < 8; ++r) qop[qb][bb][r] = (_Float16) __builtin_amdgcn_ldexpf(xq[bb][r], eq);
     }
+    BMO_PHASE(2);
     // this wave's query positions and the keys they may see (wave-uniform)
     const int wq1 = min(wq0 + QWV - 1, p.n_tok - 1);
     const int w_hi = pos0 + wq1;
@@ -813,6 +862,7 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
     // a tile pair follows every wave's multiplication of the pair before, so
     // writing a buffer NBUF positions later is safe.
     if constexpr (DIRECT) quantize_chunk();
+    BMO_PHASE(3);
     // DIRECT: the chunk's blocks go into their ring slots (pos0 + i) % n_ctx
     // while the tiles are multiplied.  Chunk key i replaces old position
     // pos0 + i - n_ctx, which only its ring tile carries (a 17th ring tile,
@@ -881,6 +931,7 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
         for (int base = 0; base < n_tiles; base += PF + 1) {
 #pragma unroll
             for (int u = 0; u <= PF; u += TPB) {
+                BMO_PHASE_LOOP();
                 if constexpr (LOADS) {
 #pragma unroll
                     for (int k = 0; k < TPB; ++k)
@@ -895,21 +946,29 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
                         fetch(raw[nxt], rawd[nxt]);
                     }
                 }
+                BMO_PHASE_LOOP();
                 lds_barrier();  // these TPB buffers are complete
+                BMO_PHASE_LOOP();
                 if constexpr (DIRECT && !LOADS) {
                     const int lim = commit_limit(base + u + TPB);
                     if (lim > i_done) commit_until(lim);
                     if (touch_on && base + u == touch_at) touch_successor();
                 }
+                BMO_PHASE_LOOP();
 #pragma unroll
                 for (int k = 0; k < TPB; ++k) compute((u + k) % NBUF, tile_of(base + u + k));
             }
         }
     };
+    BMO_PHASE(4);
     if (has_items)
         tile_loop(BoolC<true>{});
     else
         tile_loop(BoolC<false>{});
+    BMO_PHASE(5);
+#if BMO_PREFILL_PHASES
+    if (lane == 0) phase_rec[8] = (uint64_t) phase_n;
+#endif
     // (the touched value is needed by nothing; the read must not be dropped)
     asm volatile("" ::"v"(touched));
     // The loop has written every key: its last barrier publishes every ring
@@ -964,6 +1023,10 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
             }
         }
     }
+    BMO_PHASE(6);
+#if BMO_PREFILL_PHASES
+    if (lane == 0) phase_rec[7] = __builtin_amdgcn_s_memrealtime();
+#endif
 }
 
 namespace {
@@ -1014,6 +1077,16 @@ static int resident_workgroups() {
 // and ring tiles that never wrap (the per-key slots of other ring sizes do
 // not fit its register budget beside the exact block scales; those rings
 // take the staged path).
+#if BMO_PREFILL_PHASES
+// The diagnostic build's phase records (kPhaseUnits workgroups x 16 waves x
+// kPhaseRec stamps), copied to host memory after a synchronization.
+extern "C" __attribute__((visibility("default"))) int bmo_prefill_phase_stamps(void *dst, size_t bytes) {
+    if (!dst || bytes > sizeof(g_prefill_phases)) return 2;
+    if (hipDeviceSynchronize() != hipSuccess) return 8;
+    return hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_prefill_phases), bytes, 0, hipMemcpyDeviceToHost) == hipSuccess ? 0 : 8;
+}
+#endif
+
 bool prefill_is_direct(const PrefillParams &p) {
     return p.n_heads == p.n_kv && p.n_tok <= kQT && p.g.n_ctx % kTK == 0;
 }
