@@ -8,9 +8,9 @@ float64 oracle once q has large elements: q * scale * log2(e) rounded to 11
 bits, and the dequantized key (c - 8) * d rounded to 11 bits (a CPU model of
 both, D=128, 512 keys: 1-3% of query rows out of tolerance, up to 57x the
 bound, for one x30..x1000 outlier channel per block).  The kernel therefore
-scales each query row by a power of two (exact in fp16), feeds the key codes
-(c - 8) exactly, and applies each block's d and the residual query factor to
-the fp32 scores.  These tests run the query kinds of the decode range tests
+scales each query row by a power of two (exact in fp16) and applies the
+residual query factor to the fp32 scores, and feeds the key codes (c - 8)
+exactly, each block's d multiplying its product in fp32.  These tests run the query kinds of the decode range tests
 through prefill:
 
   * one outlier channel per 32-element block at x30, x100, x300, x1000 and
@@ -20,6 +20,8 @@ through prefill:
   * whole rows scaled by 2^20 (beyond fp16 after any fixed scaling), 2^-20
     and 2^-100;
   * rows whose blocks differ in scale by 2^30 from block to block;
+  * keys scaled by 2^-11 .. 2^-20 (fp16 block scales down to subnormal) or
+    2^8, with queries scaled to keep the scores' spread;
 
 at config 5's head shape (32 heads x d128, a 512-slot ring with full history,
 256-token chunks: the direct path), on the staged path with 4 query heads per
@@ -160,6 +162,36 @@ def test_prefill_random_shape_q_range(gpu, seed):
                 f"n_ctx {n_ctx} heads {n_heads}/{n_kv}")
         check_close(got[b], ref[b], what)
         m.assert_ring_equal(0, s)
+
+
+# (key exponent, query exponent): keys N(0,1) * 2^ke, queries N(0,1) * 2^qe,
+# so the scores keep a spread of about 6 log2 units while the blocks' fp16
+# scales d run from normal through subnormal (ke -16, -20) to large (ke 8).
+KEY_RANGES = [(-11, 13), (-16, 18), (-20, 22), (8, -6)]
+
+
+@pytest.mark.parametrize("ke,qe", KEY_RANGES)
+@pytest.mark.parametrize("n_kv", [32, 8])
+def test_prefill_key_scale_range(gpu, ke, qe, n_kv):
+    """Keys whose Q4_0 scales are subnormal in fp16, or large, against
+    queries scaled so that the scores still matter: each block's d must
+    reach the scores exactly (a flushed subnormal scale zeroes its keys, and
+    a d carried at reduced precision moves the scores by up to 2^-8 of their
+    size, far past the tolerance here).
+    n_kv 32: config 5's head shape on the direct path; n_kv 8: 4 query heads
+    per kv head on the staged path.  History full, 256-token chunk."""
+    n_heads, d, n_ctx, pos0, n_tok = 32, 128, 512, 1000, 256
+    m = Mirror(gpu, 1, 1, n_kv, d, n_ctx)
+    lo = pos0 - n_ctx
+    hk = oracle.normal(0x5CA10 + ke, n_ctx * n_kv * d).reshape(n_ctx, n_kv, d) * np.float32(2.0 ** ke)
+    hv = oracle.normal(0x5CA20 + ke, n_ctx * n_kv * d).reshape(n_ctx, n_kv, d)
+    m.write(0, 0, lo, hk.astype(np.float32), hv)
+    q = oracle.round_bf16(_bf16_normals(0x5CA30, (1, n_tok, n_heads, d)) * np.float32(2.0 ** qe))
+    k = oracle.round_bf16(_bf16_normals(0x5CA40, (1, n_tok, n_kv, d)) * np.float32(2.0 ** ke))
+    v = _bf16_normals(0x5CA50, (1, n_tok, n_kv, d))
+    got, ref = _prefill(gpu, m, 0, [0], [pos0], q, k, v, n_heads)
+    check_close(got, ref, f"prefill key scale 2^{ke}, q 2^{qe}, n_kv {n_kv}")
+    m.assert_ring_equal(0, 0)
 
 
 @pytest.mark.parametrize("bad", [float("nan"), float("inf"), float("-inf")])
