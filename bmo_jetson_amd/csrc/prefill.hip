@@ -1034,10 +1034,12 @@ namespace {
 // One workgroup per 256 queries of a head: 16 waves x 16 queries (QB = 1),
 // 4 waves on each SIMD (at most 128 VGPRs each), so one wave's LDS and
 // matrix latencies overlap another's work.  Against 8 waves x 32 queries
-// (QB = 2, each K/V operand read feeding two matrix instructions), measured
-// at cfg5: 95.5 vs 99.6 us (ring history full), 55.6 vs 61.1 us (empty);
-// GQA 4:1, 256 tokens: 84-85 vs 91-94 us; 512-token chunks: 91-93 vs
-// 99-100 us; head_dim 64 GQA 4:1 on an 8-slot ring: 13.9 vs 16.7 us.
+// (QB = 2, each K/V operand read feeding two matrix instructions, half the
+// LDS reads per query), both on the staged path at cfg5: 92.7-93.0 vs
+// 106.5-106.6 us (ring history full), 60.7 vs 69.1 us (empty); in an
+// earlier build also GQA 4:1, 256 tokens: 84-85 vs 91-94 us; 512-token
+// chunks: 91-93 vs 99-100 us; head_dim 64 GQA 4:1 on an 8-slot ring: 13.9
+// vs 16.7 us.
 // Smaller workgroups for short chunks (4 waves below 129 tokens) were
 // measured slower whenever the ring holds history: the window's tiles
 // dominate, and all waves share their dequantization.
