@@ -465,9 +465,9 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
     // slots, which stay cached), so the number of loads in flight is the same
     // on every path and the compiler's waits stay exact.  Depth: 3 tiles
     // with 16 waves (4 per SIMD hide the rest; at cfg5 depth 7 measured
-    // 85.7 vs 84.0 us in an earlier build and 78.4 vs 74.2 us in this one,
-    // where it spills 3 VGPRs; depth 3 spills in no instantiation), 7 with
-    // fewer.
+    // 85.7 vs 84.0 us in one earlier build and 78.4 vs 74.2 us in a later
+    // one, where it spilled 3 VGPRs; depth 3 spills in no instantiation), 7
+    // with fewer.
     constexpr int PF = QW >= 16 ? 3 : 7;
     static_assert((PF + 1) % NBUF == 0, "the unrolled slot must determine the LDS buffer");
     uint2 raw[PF + 1][IPT];
@@ -906,9 +906,10 @@ __global__ __launch_bounds__(64 * QW, QW / 4) void prefill_kernel(PrefillParams 
     // hit this XCD's L2 (64 KB a workgroup, 2 MB an XCD at cfg5; the output's
     // nontemporal stores leave the L2 to them).  A round's whole input does
     // not fit the L2, and touching the chunk's K rows too was slower (75.9
-    // vs 72.7 us).  At cfg5, against the same kernel without the touch and
-    // with plain output stores: 70.5 vs 73.2-74.2 us full history, 46.1 vs
-    // 47.0 us empty; halfway through the loop instead, 71.3-71.7 / 46.7-47.7.
+    // vs 72.7 us).  At cfg5, in the build before the exact block scales,
+    // against the same kernel without the touch and with plain output
+    // stores: 70.5 vs 73.2-74.2 us full history, 46.1 vs 47.0 us empty;
+    // halfway through the loop instead, 71.3-71.7 / 46.7-47.7.
     const int succ = (int) blockIdx.x + p.n_resident;
     const bool touch_on = DIRECT && p.n_resident > 0 && succ < (int) gridDim.x;
     constexpr int LPR = D * 2 / 128;  // 128-byte lines of a query row
