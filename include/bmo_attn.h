@@ -201,18 +201,19 @@ BMO_ATTN_API int bmo_kv_ring_append_decode_rope(bmo_kv_ring_t *ring, int layer, 
  *   q:    [n_batch][n_tok][n_heads][head_dim] bf16 (bit patterns)
  *   k, v: [n_batch][n_tok][n_kv_heads][head_dim] bf16
  *   out:  [n_batch][n_tok][n_heads][head_dim] fp32
- * Attention runs on matrix cores: K, V and the softmax weights in fp16 (K and
- * V values must lie in fp16 range, as the reference's F16 cache requires),
- * q from its bf16 values times scale * log2(e) rounded to fp16, fp32
- * accumulation.  So |q| * scale * log2(e) must stay below 65504 (|q| below
- * about 5.1e5 at head_dim 128 with the default scale); a query with a larger
- * element gets a non-finite output row, and the other queries are
- * unaffected.  With n_heads == n_kv_heads and
- * n_tok <= 256 one kernel quantizes, attends and commits; otherwise the call
- * stages the chunk's Q4_0 blocks in the ring's staging buffer (n_batch *
- * n_kv_heads stripes of n_tok slots), grown on first use with a
- * synchronization of stream; staged calls on one ring share that buffer and
- * must therefore be ordered on one stream. */
+ * Attention runs on matrix cores with scores as close as fp32 arithmetic on
+ * the bf16 q: each query row enters scaled by its own power of two (exact in
+ * fp16 whatever the row's range), K as its exact codes (c - 8) with each
+ * block's fp16 scale applied in fp32; V and the softmax weights in fp16,
+ * fp32 accumulation (K and V values must lie in fp16 range, as the
+ * reference's F16 cache requires).  A query row holding a NaN or an
+ * infinity gets a NaN output row; the other rows are unaffected.  With
+ * n_heads == n_kv_heads, n_tok <= 256 and n_ctx a multiple of 32, one kernel
+ * quantizes, attends and commits; otherwise the call stages the chunk's
+ * Q4_0 blocks in the ring's staging buffer (n_batch * n_kv_heads stripes of
+ * n_tok slots), grown on first use with a synchronization of stream; staged
+ * calls on one ring share that buffer and must therefore be ordered on one
+ * stream. */
 BMO_ATTN_API int bmo_kv_ring_prefill(bmo_kv_ring_t *ring, int layer, int n_batch,
                                      const int *session_ids, const int *pos0,
                                      int n_tok, int n_heads, const uint16_t *q,
