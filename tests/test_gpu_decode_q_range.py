@@ -10,7 +10,9 @@ against the float64 oracle for any realistic post-RoPE q, not just N(0,1):
   * one outlier channel per head at x300 (the others N(0,1));
   * blocks mixing magnitudes 1e-3 and 1e3 element by element;
   * whole heads scaled by 2^20 and 2^-20, and by 2^-100 (scores ~0);
-  * heads whose blocks differ in scale by 2^30 from block to block.
+  * heads whose blocks differ in scale by 2^30 from block to block;
+  * keys scaled by 2^-11 .. 2^-20 (fp16 block scales down to subnormal) or
+    2^8, with queries scaled to keep the scores' spread.
 
 Plain, fused and RoPE-fused decode run at BASELINE config 1's shape (H=32,
 d=128, W=512, write head at 700) and in seeded random batches; a head whose
@@ -110,6 +112,42 @@ def test_rope_cfg1_q_range(gpu, kind):
     gpu.cuda.synchronize()
     ref = m.oracle_decode(0, 0, pos, oracle.rope_interleaved(q, pos, theta), H)
     check_close(out.cpu().numpy().reshape(H, d), ref, f"rope cfg1 q={kind}")
+    m.assert_ring_equal(0, 0)
+
+
+# (key exponent, query exponent): keys N(0,1) * 2^ke, queries N(0,1) * 2^qe,
+# so the scores keep a spread of about 6 log2 units while the blocks' fp16
+# scales d run from normal through subnormal (ke -16, -20) to large (ke 8).
+KEY_RANGES = [(-11, 13), (-16, 18), (-20, 22), (8, -6)]
+
+
+@pytest.mark.parametrize("ke,qe", KEY_RANGES)
+@pytest.mark.parametrize("fused", [False, True])
+def test_decode_cfg1_key_scale_range(gpu, ke, qe, fused):
+    """Keys whose Q4_0 scales are subnormal in fp16, or large, against
+    queries scaled so that the scores still matter: each block's d must
+    reach the scores exactly (a flushed subnormal scale zeroes its keys).
+    Config 1's shape, plain decode and fused append + decode."""
+    pos, H, d, n_ctx = 700, 32, 128, 512
+    m = Mirror(gpu, 1, 1, H, d, n_ctx)
+    lo = pos + 1 - n_ctx
+    n = pos - lo + (0 if fused else 1)
+    hk = oracle.normal(0x4B10 + ke, n * H * d).reshape(n, H, d) * np.float32(2.0 ** ke)
+    hv = oracle.normal(0x4B20 + ke, n * H * d).reshape(n, H, d)
+    m.write(0, 0, lo, hk.astype(np.float32), hv)
+    q = oracle.normal(0x4B30, H * d) * np.float32(2.0 ** qe)
+    out = gpu.full((H * d,), float("nan"), dtype=gpu.float32, device="cuda")
+    if fused:
+        k = oracle.normal(0x4B40, H * d) * np.float32(2.0 ** ke)
+        v = oracle.normal(0x4B50, H * d)
+        m.ring.append_decode(0, _i32(gpu, [pos]), m.dev(q), m.dev(k), m.dev(v), out, H,
+                             stream=m.stream)
+        m.oracle_append(0, 0, pos, k, v)
+    else:
+        m.ring.decode(0, _i32(gpu, [pos]), m.dev(q), out, H, stream=m.stream)
+    gpu.cuda.synchronize()
+    check_close(out.cpu().numpy().reshape(H, d), m.oracle_decode(0, 0, pos, q, H),
+                f"{'fused' if fused else 'plain'} decode key scale 2^{ke}, q 2^{qe}")
     m.assert_ring_equal(0, 0)
 
 
